@@ -1,0 +1,204 @@
+"""Benchmark: one-GPU training step of the reference 125M GPT (BASELINE config D).
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+Workload: 12 layers, d_model 768, 12 heads x 64, GELU MLP 3072, vocab 50304,
+seq 1024, global batch 128 sequences as 4 micro-batches of 32, AdamW
+(base LR 2^-8, betas 0.9/0.95, wd 0.1), bf16 compute with float32 master
+weights, synthetic uniform tokens from numpy seed 2, random-normal init
+(std 0.02) — the full step (forward, backward, AdamW) every iteration.
+All token batches are resident in HBM before the timed region.
+
+``value`` is training tokens/s.  ``roofline`` describes the fused linear
+cross-entropy (the largest hand-written MFMA kernel of the step), timed live
+with HIP events on the launch stream; ``roofline_attn_bwd`` does the same for
+the flash-attention backward.  ``cpu_baseline`` times the CPU restatement of
+the reference step (``oracle/``) on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gpt-speedrun-tpu_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "train tokens/s at 125M S=1024; attn-bwd + FLCE TFLOP/s as % of bf16 MFMA peak"
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--micro-batch", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="approximate CPU-baseline budget")
+    return ap.parse_args()
+
+
+def attn_bwd_flops(batch, heads, seq, head_dim):
+    """Causal-exact algorithmic FLOPs of one attention backward (dV, dP, dK, dQ)."""
+    visible = seq * (seq + 1) // 2
+    return 8 * batch * heads * head_dim * visible
+
+
+def flce_flops(n, d, vocab):
+    """Forward + backward algorithmic FLOPs of the LM-head cross-entropy (6 N d V)."""
+    return 6 * n * d * vocab
+
+
+def step_flops(layers, d, seq, tokens, vocab, mlp=4):
+    """Causal-exact training FLOPs of one step (3x forward)."""
+    per_token = 2 * (12 * d * d if mlp == 4 else (4 + 2 * mlp) * d * d) * layers  # qkv, out, up, down
+    per_token += 2 * d * vocab  # LM head
+    attn = 4 * d * (seq + 1) / 2 * layers  # QK^T and PV over the causal prefix, per token
+    return 3 * (per_token + attn) * tokens
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Time the oracle (CPU restatement) on config D with a bounded batch:
+    forward+backward of ``b`` sequences and one AdamW update over all params,
+    extrapolated to the 128-sequence global batch."""
+
+    from oracle import model as om
+    from oracle import optim as oopt
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cfg = om.baseline_config("D", steps=1000)
+    state = om.init_state(cfg, 0)
+    win = om.synthetic_windows(2, 1, 1, cfg.seq_len, cfg.vocab_size)[0]
+    x, y = torch.from_numpy(win[:, :-1]), torch.from_numpy(win[:, 1:])
+    leaves = {k: v.detach().requires_grad_(True) for k, v in state.params.items()}
+    t0 = time.perf_counter()
+    loss = om.cross_entropy(leaves, x, y, cfg)
+    grads = torch.autograd.grad(loss, list(leaves.values()))
+    t_fb = time.perf_counter() - t0
+    g = {k: gr.float() for k, gr in zip(leaves.keys(), grads)}
+    t0 = time.perf_counter()
+    oopt.adamw_step(state.params, g, state.m, state.v, 1, cfg.optimizer)
+    t_adam = time.perf_counter() - t0
+    step_s = 128 * t_fb + t_adam
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {
+        "value": round(128 * 1024 / step_s, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU restatement of reference semantics (oracle/, torch-CPU fp32 math with bf16 rounding) on "
+                   f"config D: fwd+bwd of 1 sequence x 1024 tokens ({t_fb:.2f} s) and one AdamW update over "
+                   f"162.3M params ({t_adam:.2f} s), extrapolated to 128 sequences + 1 update; {cpu}"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU (--gpus > 1) is not implemented",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+
+    cfg = GPTConfig(layers=12, heads=12, d_model=768, mlp_mult=4, vocab_size=50304, semantic_vocab_size=50304,
+                    seq_len=1024, batch_size=128, micro_batch_size=args.micro_batch,
+                    optimizer=OptimizerConfig(learning_rate=2.0 ** -8, steps=1000, warmup_steps=100))
+    total = args.warmup + args.steps
+    trainer = GPTTrainer(cfg, seed=0, history_steps=total)
+    rng = np.random.default_rng(2)
+    windows = torch.from_numpy(rng.integers(0, cfg.vocab_size, size=(total, cfg.batch_size, cfg.seq_len + 1),
+                                            dtype=np.int32)).cuda()
+    xs = [windows[i, :, :-1].contiguous() for i in range(total)]
+    ys = [windows[i, :, 1:].contiguous() for i in range(total)]
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        trainer.train_step(xs[i], ys[i])
+    torch.cuda.synchronize()
+
+    trainer.timers = {}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(args.warmup, total):
+        trainer.train_step(xs[i], ys[i])
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(end)
+    ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
+    tokens_per_step = cfg.batch_size * cfg.seq_len
+    value = tokens_per_step / (ms_per_step / 1e3)
+
+    def avg_ms(name):
+        ev = trainer.timers.get(name, [])
+        return sum(s.elapsed_time(e) for s, e in ev) / max(len(ev), 1), len(ev)
+
+    n_micro = cfg.batch_size // cfg.micro_batch_size
+    mb_tokens = cfg.micro_batch_size * cfg.seq_len
+    # FLCE: one forward + one backward launch per micro-batch; report per micro-batch (fwd+bwd).
+    flce_ms_launch, flce_n = avg_ms("flce")
+    flce_ms = 2 * flce_ms_launch
+    flce_tf = flce_flops(mb_tokens, cfg.d_model, cfg.vocab_size) / (flce_ms / 1e3) / 1e12
+    ab_ms, _ = avg_ms("attn_bwd")
+    ab_tf = attn_bwd_flops(cfg.micro_batch_size, cfg.heads, cfg.seq_len, cfg.head_dim) / (ab_ms / 1e3) / 1e12
+    af_ms, _ = avg_ms("attn_fwd")
+    adam_ms, _ = avg_ms("adamw")
+    adam_gbs = 28 * trainer.arena.numel() / (adam_ms / 1e3) / 1e9
+    hist = trainer.history_rows()
+    total_flops = step_flops(cfg.layers, cfg.d_model, cfg.seq_len, tokens_per_step, cfg.vocab_size)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config D: reference GPT 125M (12x768, 12 heads x 64, mlp 3072, vocab 50304) "
+                               "full train step, S=1024, global batch 128 as 4 micro-batches of 32, AdamW",
+                   "global_batch": cfg.batch_size, "micro_batch": cfg.micro_batch_size, "seq_len": cfg.seq_len,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"kernel": "flce (fused LM-head cross-entropy fwd+bwd, per 32x1024-token micro-batch)",
+                     "bound": "mfma", "achieved": round(flce_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flce_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "ms": round(flce_ms, 3), "algorithmic_flops": flce_flops(mb_tokens, cfg.d_model,
+                                                                              cfg.vocab_size)},
+        "roofline_attn_bwd": {"kernel": "attn_bwd (B32 H12 S1024 D64 causal)", "bound": "mfma",
+                              "achieved": round(ab_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(ab_tf / MFMA_BF16_PEAK_TFLOPS, 4), "ms": round(ab_ms, 3)},
+        "step_tflops": round(total_flops / (ms_per_step / 1e3) / 1e12, 1),
+        "step_mfu": round(total_flops / (ms_per_step / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "attn_fwd_ms": round(af_ms, 3),
+        "adamw": {"ms": round(adam_ms, 3), "achieved_GBps": round(adam_gbs, 1), "peak_GBps": 8000},
+        "loss_first_last": [float(hist[0, 0]), float(hist[-1, 0])],
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

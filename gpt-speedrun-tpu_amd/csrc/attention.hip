@@ -1,0 +1,605 @@
+// Causal flash attention for gfx950: bf16 MFMA (v_mfma_f32_32x32x16_bf16),
+// fp32 online softmax in the exp2 domain, LDS-staged K/V tiles.
+//
+// Semantics follow rig/kernels/tpu_flash_attention.py:
+//   forward  (:236-348)  O = softmax(scale*QK^T masked) V, LSE = log sum exp
+//   dQ       (:479-575)  dQ = (P o (dO V^T - Delta)) * scale  K
+//   dK/dV    (:578-701)  dV = P^T dO,  dK = dS^T Q
+// with P recomputed from the saved LSE, Delta = rowsum(O o dO), and the
+// probability / dS operands rounded to bf16 before their products.
+//
+// Forward mapping: a workgroup owns 128 queries (4 waves x 32).  Each wave
+// computes S^T = K Q^T so that MFMA lane l holds query l%32 and 16 keys: the
+// row max/sum are lane-local (+ one xor-32 exchange) and P^T is already the
+// B operand of O^T = V^T P^T, so probabilities never leave registers.
+//
+// Backward mapping: a workgroup owns 128 keys (4 waves x 32) and walks the
+// causal query blocks (64 queries per step).  Each wave computes S = Q K^T and
+// dP = dO V^T with lane l holding key l%32, accumulates dV^T += dO^T P and
+// dK^T += Q^T dS in registers, and publishes bf16 dS to LDS; the workgroup
+// then forms dQ = dS K (all 128 keys) and adds it to an fp32 accumulator with
+// atomics.  A last pass rounds dQ to bf16.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlockM = 128;  // forward: queries per workgroup
+constexpr int kBlockN = 64;   // forward: keys per LDS tile
+constexpr int kBwdN = 128;    // backward: keys per workgroup
+constexpr int kBwdM = 64;     // backward: queries per step
+constexpr float kMinusBig = -1.0e30f;
+
+struct View {
+  const bf16* p;
+  int64_t sb, sh, ss;
+  __device__ __forceinline__ const bf16* row(int b, int h, int s) const { return p + b * sb + h * sh + s * ss; }
+};
+struct MutView {
+  bf16* p;
+  int64_t sb, sh, ss;
+  __device__ __forceinline__ bf16* row(int b, int h, int s) const { return p + b * sb + h * sh + s * ss; }
+};
+
+// Workgroup id -> (batch*head, block) such that all blocks of one (b, h) run on
+// the same XCD (workgroups are dispatched round-robin over the 8 XCDs), which
+// keeps that head's K/V (forward) or Q/dO/dQ (backward) in one L2.
+__device__ __forceinline__ void xcd_map(int id, int nblocks, int bh_total, int& bh, int& blk) {
+  if ((bh_total & 7) == 0) {
+    int xcd = id & 7, slot = id >> 3;
+    bh = (slot / nblocks) * 8 + xcd;
+    blk = slot % nblocks;
+  } else {
+    bh = id / nblocks;
+    blk = id % nblocks;
+  }
+}
+
+// ============================================================================
+// Forward
+// ============================================================================
+template <int D>
+__global__ void __launch_bounds__(256, 2)
+    attn_fwd_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
+                    int B, int H, int S, float scale_log2) {
+  constexpr int KS = D + 8;        // K tile row stride (elements)
+  constexpr int VS = kBlockN + 4;  // V^T tile row stride
+  constexpr int KC = D / 16;       // 16-wide k-chunks over head_dim
+  constexpr int DB = D / 32;       // 32-wide d blocks of the output
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][kBlockN * KS];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * VS];
+
+  const int nq = (S + kBlockM - 1) / kBlockM;
+  int bh, qb;
+  xcd_map(blockIdx.x, nq, B * H, bh, qb);
+  qb = nq - 1 - qb;  // heaviest (longest causal prefix) first
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int q0 = qb * kBlockM;
+  const int qw0 = q0 + wave * 32;
+  const int my_q = qw0 + l32;
+  const int last_q = min(q0 + kBlockM, S) - 1;
+  const int ntiles = last_q / kBlockN + 1;
+
+  // Q^T operand: lane holds query my_q, d = 16kc + 8hl + j.
+  bf16x8 qreg[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    if (my_q < S)
+      qreg[kc] = *reinterpret_cast<const bf16x8*>(Q.row(b, h, my_q) + 16 * kc + 8 * hl);
+    else
+      qreg[kc] = bf16x8{};
+  }
+  const int seg_q = (seg && my_q < S) ? seg[(size_t)b * S + my_q] : 0;
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  float m_run = kMinusBig, l_run = 0.f;
+
+  // Global -> register staging of one K/V tile: 64 keys x D, 16 B per load.
+  constexpr int kLoads = kBlockN * D / 8 / 256;  // 16-byte chunks per thread
+  bf16x8 kst[kLoads], vst[kLoads];
+  auto load_tile = [&](int kv0) {
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) {
+      int idx = tid + 256 * r;
+      int key = idx / (D / 8), dc = (idx % (D / 8)) * 8;
+      if (kv0 + key < S) {
+        kst[r] = *reinterpret_cast<const bf16x8*>(K.row(b, h, kv0 + key) + dc);
+        vst[r] = *reinterpret_cast<const bf16x8*>(V.row(b, h, kv0 + key) + dc);
+      } else {
+        kst[r] = bf16x8{};
+        vst[r] = bf16x8{};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) {
+      int idx = tid + 256 * r;
+      int key = idx / (D / 8), dc = (idx % (D / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(&Ks[buf][key * KS + dc]) = kst[r];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Vt[buf][(dc + j) * VS + key] = vst[r][j];
+    }
+  };
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int kv0 = it * kBlockN;
+    if (it + 1 < ntiles) load_tile(kv0 + kBlockN);
+
+    if (kv0 <= qw0 + 31) {  // some key of this tile is visible to this wave
+      f32x16 s[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        s[sb] = f32x16{};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[buf][(32 * sb + l32) * KS + 16 * kc + 8 * hl]);
+          s[sb] = mfma32(a, qreg[kc], s[sb]);
+        }
+      }
+      const bool need_mask = (kv0 + kBlockN - 1 > qw0) || (kv0 + kBlockN > S) || seg;
+      float mloc = kMinusBig;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float x = s[sb][i] * scale_log2;
+          if (need_mask) {
+            int key = kv0 + 32 * sb + 8 * (i >> 2) + 4 * hl + (i & 3);
+            bool vis = key <= my_q && key < S;
+            if (seg && vis) vis = seg[(size_t)b * S + key] == seg_q;
+            x = vis ? x : -INFINITY;
+          }
+          s[sb][i] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      float lsum = 0.f;
+      bf16x8 pb[4];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float p = fast_exp2(s[sb][8 * c2 + j] - m_new);
+            lsum += p;
+            pb[2 * sb + c2][j] = (bf16)p;
+          }
+        }
+      }
+      l_run = l_run * alpha + lsum;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+      }
+      // O^T += V^T P^T over the tile's 4 key chunks of 16.
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bf16* row = &Vt[buf][(32 * db + l32) * VS + 16 * c + 4 * hl];
+          bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
+          bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8);
+          bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          acc[db] = mfma32(a, pb[c], acc[db]);
+        }
+      }
+    }
+
+    if (it + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (my_q < S) {
+    const float inv = 1.0f / l_tot;
+    bf16* orow = O.row(b, h, my_q);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16x4 o4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o4[t] = (bf16)(acc[db][4 * r + t] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * db + 8 * r + 4 * hl) = o4;
+      }
+    }
+    if (hl == 0) lse[((size_t)b * H + h) * S + my_q] = (m_run + __log2f(l_tot)) * GPTRIG_LN2;
+  }
+}
+
+// ============================================================================
+// Backward
+// ============================================================================
+
+// Delta = rowsum(float(O) * float(dO)) (tpu_flash_attention.py:532-535) and a
+// zeroed fp32 dQ accumulator.  8 lanes per row.
+template <int D>
+__global__ void attn_bwd_pre_kernel(View O, View dO, float* __restrict__ delta, float* __restrict__ dq_acc, int B,
+                                    int H, int S) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = t >> 3;
+  const int part = t & 7;
+  if (row >= (int64_t)B * H * S) return;
+  const int s = (int)(row % S);
+  const int bh = (int)(row / S);
+  const int b = bh / H, h = bh % H;
+  const bf16* o = O.row(b, h, s);
+  const bf16* g = dO.row(b, h, s);
+  float acc = 0.f;
+#pragma unroll
+  for (int c = part; c < D / 8; c += 8) {
+    bf16x8 ov = *reinterpret_cast<const bf16x8*>(o + 8 * c);
+    bf16x8 gv = *reinterpret_cast<const bf16x8*>(g + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += (float)ov[j] * (float)gv[j];
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (part == 0) delta[row] = acc;
+  float* dq = dq_acc + row * D;
+#pragma unroll
+  for (int c = part; c < D / 4; c += 8) *reinterpret_cast<f32x4*>(dq + 4 * c) = f32x4{};
+}
+
+template <int D>
+__global__ void __launch_bounds__(256, 2)
+    attn_bwd_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse, const float* __restrict__ delta,
+                    const int32_t* __restrict__ seg, float* __restrict__ dq_acc, MutView dK, MutView dV, int B, int H,
+                    int S, float scale, float scale_log2) {
+  constexpr int KC = D / 16;
+  constexpr int DB = D / 32;
+  constexpr int QS = D + 8;        // Q / dO row stride
+  constexpr int TS = kBwdM + 4;    // Q^T / dO^T row stride
+  constexpr int SS = kBwdN + 8;    // dS row stride
+  constexpr int KTS = kBwdN + 8;   // K^T row stride
+  __shared__ __attribute__((aligned(16))) bf16 Qs[kBwdM * QS];
+  __shared__ __attribute__((aligned(16))) bf16 dOs[kBwdM * QS];
+  __shared__ __attribute__((aligned(16))) bf16 Qt[D * TS];
+  __shared__ __attribute__((aligned(16))) bf16 dOt[D * TS];
+  __shared__ __attribute__((aligned(16))) bf16 dSs[kBwdM * SS];
+  __shared__ __attribute__((aligned(16))) bf16 Kt[D * KTS];
+  __shared__ float lse_s[kBwdM], delta_s[kBwdM];
+  __shared__ int seg_s[kBwdM];
+
+  const int nkv = (S + kBwdN - 1) / kBwdN;
+  int bh, kb;
+  xcd_map(blockIdx.x, nkv, B * H, bh, kb);
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int k0 = kb * kBwdN;
+  const int kw0 = k0 + 32 * wave;
+  const int my_k = kw0 + l32;
+  const bool k_ok = my_k < S;
+
+  // The wave's own keys as B operands (N = key = lane%32, k = d).
+  bf16x8 kreg[KC], vreg[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    if (k_ok) {
+      kreg[kc] = *reinterpret_cast<const bf16x8*>(K.row(b, h, my_k) + 16 * kc + 8 * hl);
+      vreg[kc] = *reinterpret_cast<const bf16x8*>(V.row(b, h, my_k) + 16 * kc + 8 * hl);
+    } else {
+      kreg[kc] = bf16x8{};
+      vreg[kc] = bf16x8{};
+    }
+  }
+  const int seg_k = (seg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
+
+  // K^T of the workgroup's 128 keys for the dQ product.
+  for (int idx = tid; idx < kBwdN * D / 8; idx += 256) {
+    int key = idx / (D / 8), dc = (idx % (D / 8)) * 8;
+    bf16x8 kv = bf16x8{};
+    if (k0 + key < S) kv = *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + key) + dc);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Kt[(dc + j) * KTS + key] = kv[j];
+  }
+
+  f32x16 dv_acc[DB], dk_acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dv_acc[db] = f32x16{};
+    dk_acc[db] = f32x16{};
+  }
+
+  const float* lse_bh = lse + (size_t)bh * S;
+  const float* delta_bh = delta + (size_t)bh * S;
+  float* dq_bh = dq_acc + (size_t)bh * S * D;
+
+  constexpr int kLoads = kBwdM * D / 8 / 256;
+  bf16x8 qst[kLoads], gst[kLoads];
+  float lse_st = 0.f, delta_st = 0.f;
+  int seg_st = 0;
+  auto load_q = [&](int qq0) {
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) {
+      int idx = tid + 256 * r;
+      int qi = idx / (D / 8), dc = (idx % (D / 8)) * 8;
+      if (qq0 + qi < S) {
+        qst[r] = *reinterpret_cast<const bf16x8*>(Q.row(b, h, qq0 + qi) + dc);
+        gst[r] = *reinterpret_cast<const bf16x8*>(dO.row(b, h, qq0 + qi) + dc);
+      } else {
+        qst[r] = bf16x8{};
+        gst[r] = bf16x8{};
+      }
+    }
+    if (tid < kBwdM) {
+      int q = qq0 + tid;
+      lse_st = q < S ? lse_bh[q] * GPTRIG_LOG2E : 0.f;
+      delta_st = q < S ? delta_bh[q] : 0.f;
+      seg_st = (seg && q < S) ? seg[(size_t)b * S + q] : 0;
+    }
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) {
+      int idx = tid + 256 * r;
+      int qi = idx / (D / 8), dc = (idx % (D / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(&Qs[qi * QS + dc]) = qst[r];
+      *reinterpret_cast<bf16x8*>(&dOs[qi * QS + dc]) = gst[r];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        Qt[(dc + j) * TS + qi] = qst[r][j];
+        dOt[(dc + j) * TS + qi] = gst[r][j];
+      }
+    }
+    if (tid < kBwdM) {
+      lse_s[tid] = lse_st;
+      delta_s[tid] = delta_st;
+      seg_s[tid] = seg_st;
+    }
+  };
+
+  const int qb_first = k0 / kBwdM;
+  const int nqb = (S + kBwdM - 1) / kBwdM;
+  load_q(qb_first * kBwdM);
+
+  for (int qb = qb_first; qb < nqb; ++qb) {
+    const int qq0 = qb * kBwdM;
+    store_q();
+    __syncthreads();  // (A) Q, dO, transposes, lse, delta published
+    if (qb + 1 < nqb) load_q(qq0 + kBwdM);
+
+    const bool wave_active = kw0 <= qq0 + kBwdM - 1 && kw0 < S;
+    const bool need_mask = (qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || seg;
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      if (!wave_active) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          int qi = 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
+          dSs[qi * SS + 32 * wave + l32] = (bf16)0.f;
+        }
+        continue;
+      }
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        bf16x8 aq = *reinterpret_cast<const bf16x8*>(&Qs[(32 * qs + l32) * QS + 16 * kc + 8 * hl]);
+        bf16x8 ag = *reinterpret_cast<const bf16x8*>(&dOs[(32 * qs + l32) * QS + 16 * kc + 8 * hl]);
+        sacc = mfma32(aq, kreg[kc], sacc);
+        pacc = mfma32(ag, vreg[kc], pacc);
+      }
+      bf16x8 pb[2], db8[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int qi = 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
+        float p = fast_exp2(sacc[i] * scale_log2 - lse_s[qi]);
+        if (need_mask) {
+          const int q = qq0 + qi;
+          bool vis = my_k <= q && q < S && k_ok;
+          if (seg && vis) vis = seg_s[qi] == seg_k;
+          p = vis ? p : 0.f;
+        }
+        float ds = p * (pacc[i] - delta_s[qi]) * scale;
+        pb[i >> 3][i & 7] = (bf16)p;
+        bf16 dsb = (bf16)ds;
+        db8[i >> 3][i & 7] = dsb;
+        dSs[qi * SS + 32 * wave + l32] = dsb;
+      }
+      // dV^T += dO^T P ; dK^T += Q^T dS   (contraction over this sub-block's 32 queries)
+#pragma unroll
+      for (int dbk = 0; dbk < DB; ++dbk) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int col = 32 * qs + 16 * c + 4 * hl;
+          const bf16* grow = &dOt[(32 * dbk + l32) * TS + col];
+          const bf16* qrow = &Qt[(32 * dbk + l32) * TS + col];
+          bf16x4 glo = *reinterpret_cast<const bf16x4*>(grow);
+          bf16x4 ghi = *reinterpret_cast<const bf16x4*>(grow + 8);
+          bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qrow);
+          bf16x4 qhi = *reinterpret_cast<const bf16x4*>(qrow + 8);
+          bf16x8 ag = {glo[0], glo[1], glo[2], glo[3], ghi[0], ghi[1], ghi[2], ghi[3]};
+          bf16x8 aq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+          dv_acc[dbk] = mfma32(ag, pb[c], dv_acc[dbk]);
+          dk_acc[dbk] = mfma32(aq, db8[c], dk_acc[dbk]);
+        }
+      }
+    }
+    __syncthreads();  // (B) dS published
+
+    // dQ tile of this wave: queries 32*(wave/2).., d 32*(wave%2).. over all 128 keys.
+    {
+      const int qs = wave >> 1;
+      f32x16 dq_tile[DB / 2 > 0 ? DB / 2 : 1];
+      // For D=64 each wave owns one 32x32 tile; for D=128 two (d blocks wave%2 and wave%2+2).
+#pragma unroll
+      for (int t = 0; t < (DB + 1) / 2; ++t) dq_tile[t] = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < kBwdN / 16; ++kc) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&dSs[(32 * qs + l32) * SS + 16 * kc + 8 * hl]);
+#pragma unroll
+        for (int t = 0; t < (DB + 1) / 2; ++t) {
+          const int dblk = (wave & 1) + 2 * t;
+          bf16x8 bk = *reinterpret_cast<const bf16x8*>(&Kt[(32 * dblk + l32) * KTS + 16 * kc + 8 * hl]);
+          dq_tile[t] = mfma32(a, bk, dq_tile[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < (DB + 1) / 2; ++t) {
+        const int dcol = 32 * ((wave & 1) + 2 * t) + l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int q = qq0 + 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
+          if (q < S) atomicAdd(dq_bh + (size_t)q * D + dcol, dq_tile[t][i]);
+        }
+      }
+    }
+  }
+
+  if (k_ok) {
+    bf16* dvrow = dV.row(b, h, my_k);
+    bf16* dkrow = dK.row(b, h, my_k);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16x4 v4, k4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          v4[t] = (bf16)dv_acc[db][4 * r + t];
+          k4[t] = (bf16)dk_acc[db][4 * r + t];
+        }
+        *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * r + 4 * hl) = v4;
+        *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * r + 4 * hl) = k4;
+      }
+    }
+  }
+}
+
+template <int D>
+__global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView dQ, int B, int H, int S) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = t / (D / 8);
+  const int c = (int)(t % (D / 8));
+  if (row >= (int64_t)B * H * S) return;
+  const int s = (int)(row % S);
+  const int bh = (int)(row / S);
+  const float* src = dq_acc + row * D + 8 * c;
+  f32x4 a = *reinterpret_cast<const f32x4*>(src);
+  f32x4 bb = *reinterpret_cast<const f32x4*>(src + 4);
+  bf16x8 o = {(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3], (bf16)bb[0], (bf16)bb[1], (bf16)bb[2], (bf16)bb[3]};
+  *reinterpret_cast<bf16x8*>(dQ.row(bh / H, bh % H, s) + 8 * c) = o;
+}
+
+bool strides_ok(const int64_t* st, int n) {
+  // Row starts must stay 16-byte aligned for the vector loads.
+  for (int i = 0; i < 3 * n; ++i)
+    if (st[i] < 0 || (st[i] & 7)) return false;
+  return true;
+}
+
+void default_strides(int64_t* st, int n, int H, int S, int D) {
+  for (int i = 0; i < n; ++i) {
+    st[3 * i + 0] = (int64_t)H * S * D;
+    st[3 * i + 1] = (int64_t)S * D;
+    st[3 * i + 2] = D;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int gptrig_attn_fwd(const void* q, const void* k, const void* v, const int32_t* segment_ids, void* o, float* lse,
+                    int batch, int heads, int seq, int head_dim, const int64_t* strides, float softmax_scale,
+                    void* stream) {
+  if (!q || !k || !v || !o || !lse) return GPTRIG_E_NULL;
+  if (batch <= 0 || heads <= 0 || seq <= 0 || head_dim <= 0) return GPTRIG_E_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return GPTRIG_E_UNSUPPORTED;
+  if (!(softmax_scale > 0.f)) return GPTRIG_E_SHAPE;
+  int64_t st[12];
+  if (strides) {
+    for (int i = 0; i < 12; ++i) st[i] = strides[i];
+  } else {
+    default_strides(st, 4, heads, seq, head_dim);
+  }
+  if (!strides_ok(st, 4)) return GPTRIG_E_SHAPE;
+  View Q{(const bf16*)q, st[0], st[1], st[2]}, K{(const bf16*)k, st[3], st[4], st[5]},
+      V{(const bf16*)v, st[6], st[7], st[8]};
+  MutView O{(bf16*)o, st[9], st[10], st[11]};
+  const int nq = (seq + kBlockM - 1) / kBlockM;
+  const long long grid = (long long)batch * heads * nq;
+  const float sl2 = softmax_scale * GPTRIG_LOG2E;
+  hipStream_t s = (hipStream_t)stream;
+  if (head_dim == 64)
+    attn_fwd_kernel<64><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
+  else
+    attn_fwd_kernel<128><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+size_t gptrig_attn_bwd_workspace_bytes(int batch, int heads, int seq, int head_dim) {
+  const size_t rows = (size_t)batch * heads * seq;
+  const size_t delta = (rows * sizeof(float) + 255) & ~(size_t)255;
+  return delta + rows * head_dim * sizeof(float);
+}
+
+int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                    const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace,
+                    size_t workspace_bytes, int batch, int heads, int seq, int head_dim, const int64_t* strides,
+                    float softmax_scale, void* stream) {
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !workspace) return GPTRIG_E_NULL;
+  if (batch <= 0 || heads <= 0 || seq <= 0 || head_dim <= 0) return GPTRIG_E_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return GPTRIG_E_UNSUPPORTED;
+  if (!(softmax_scale > 0.f)) return GPTRIG_E_SHAPE;
+  if (workspace_bytes < gptrig_attn_bwd_workspace_bytes(batch, heads, seq, head_dim)) return GPTRIG_E_WORKSPACE;
+  if ((uintptr_t)workspace & 15) return GPTRIG_E_SHAPE;
+  int64_t st[24];
+  if (strides) {
+    for (int i = 0; i < 24; ++i) st[i] = strides[i];
+  } else {
+    default_strides(st, 8, heads, seq, head_dim);
+  }
+  if (!strides_ok(st, 8)) return GPTRIG_E_SHAPE;
+  View Q{(const bf16*)q, st[0], st[1], st[2]}, K{(const bf16*)k, st[3], st[4], st[5]},
+      V{(const bf16*)v, st[6], st[7], st[8]}, O{(const bf16*)o, st[9], st[10], st[11]},
+      dO{(const bf16*)dout, st[12], st[13], st[14]};
+  MutView dQ{(bf16*)dq, st[15], st[16], st[17]}, dK{(bf16*)dk, st[18], st[19], st[20]},
+      dV{(bf16*)dv, st[21], st[22], st[23]};
+  const size_t rows = (size_t)batch * heads * seq;
+  float* delta = (float*)workspace;
+  float* dq_acc = (float*)((char*)workspace + ((rows * sizeof(float) + 255) & ~(size_t)255));
+  hipStream_t s = (hipStream_t)stream;
+  const int nkv = (seq + kBwdN - 1) / kBwdN;
+  const long long grid = (long long)batch * heads * nkv;
+  const float sl2 = softmax_scale * GPTRIG_LOG2E;
+  if (head_dim == 64) {
+    attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
+                                                                                seq);
+    GPTRIG_CHECK_LAUNCH();
+    attn_bwd_kernel<64><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV, batch,
+                                                       heads, seq, softmax_scale, sl2);
+    GPTRIG_CHECK_LAUNCH();
+    attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq);
+  } else {
+    attn_bwd_pre_kernel<128><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
+                                                                                 seq);
+    GPTRIG_CHECK_LAUNCH();
+    attn_bwd_kernel<128><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV, batch,
+                                                        heads, seq, softmax_scale, sl2);
+    GPTRIG_CHECK_LAUNCH();
+    attn_dq_convert_kernel<128><<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq);
+  }
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+}  // extern "C"

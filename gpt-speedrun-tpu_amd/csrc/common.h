@@ -1,0 +1,64 @@
+// Shared device/host helpers for the gptrig gfx950 kernels.
+//
+// bf16 storage is the clang `__bf16` type: conversions from float compile to
+// gfx950's v_cvt_pk_bf16_f32 (round-to-nearest-even), the same rounding as
+// jax's astype(bfloat16).  MFMA operands are 8-wide bf16 vectors.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gptrig.h"
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+#define GPTRIG_LOG2E 1.4426950408889634f
+#define GPTRIG_LN2 0.6931471805599453f
+
+#define GPTRIG_CHECK_LAUNCH()                                   \
+  do {                                                          \
+    if (hipGetLastError() != hipSuccess) return GPTRIG_E_LAUNCH; \
+  } while (0)
+
+__device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
+__device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }
+
+// 32x32x16 bf16 MFMA: A rows = lane%32 (8 k-values per lane), B cols = lane%32,
+// C: lane holds column lane%32, rows 8*(i/4) + 4*(lane/32) + (i%4), i = 0..15.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// 16x16x32 bf16 MFMA: A rows = lane%16, B cols = lane%16,
+// C: lane holds column lane%16, rows 4*(lane/16) + i, i = 0..3.
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Pack 8 floats into an MFMA bf16 operand.
+__device__ __forceinline__ bf16x8 pack8(const float* v) {
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = (bf16)v[j];
+  return r;
+}
+
+static inline int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }

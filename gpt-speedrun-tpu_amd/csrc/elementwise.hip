@@ -1,0 +1,567 @@
+// HBM-bound passes of the training step: RMSNorm, GELU(tanh), interleaved RoPE,
+// embedding gather/scatter, fused AdamW with the gradient-norm reduction, and
+// small reductions.  Every kernel streams 16-byte vectors where the shape
+// allows and falls back to a scalar tail otherwise.
+#include "common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int kWave = 64;
+
+// ----------------------------------------------------------------------------
+// RMSNorm  (rig/nn.py:26-33)
+//   n  = bf16(x * rsqrt(mean(x^2) + 1e-5))      statistic in fp32
+//   y  = bf16(n * scale_bf16)
+// One wave per row; rstd saved for the backward.
+// ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ scale,
+                                                          bf16* __restrict__ y, float* __restrict__ rstd, int rows,
+                                                          int d) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const bf16* xr = x + (size_t)row * d;
+  bf16* yr = y + (size_t)row * d;
+  float ss = 0.f;
+  if ((d & 7) == 0) {
+    for (int c = lane; c < d / 8; c += kWave) {
+      bf16x8 v = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float f = (float)v[j];
+        ss += f * f;
+      }
+    }
+  } else {
+    for (int c = lane; c < d; c += kWave) {
+      float f = (float)xr[c];
+      ss += f * f;
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)d + 1.0e-5f);
+  if (lane == 0 && rstd) rstd[row] = r;
+  if ((d & 7) == 0) {
+    for (int c = lane; c < d / 8; c += kWave) {
+      bf16x8 v = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
+      bf16x8 s = *reinterpret_cast<const bf16x8*>(scale + 8 * c);
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float n = (float)(bf16)((float)v[j] * r);
+        o[j] = (bf16)(n * (float)s[j]);
+      }
+      *reinterpret_cast<bf16x8*>(yr + 8 * c) = o;
+    }
+  } else {
+    for (int c = lane; c < d; c += kWave) {
+      float n = (float)(bf16)((float)xr[c] * r);
+      yr[c] = (bf16)(n * (float)scale[c]);
+    }
+  }
+}
+
+// Backward of rms_norm by the chain rule through the two roundings:
+//   dn = bf16(dy * scale)                       (cotangent of the bf16 product)
+//   dx = r*dn - (r^3/d) * x * sum_j(dn_j x_j)   (fp32), rounded to bf16
+//   dx += dresidual (bf16 add), if given
+//   dscale_partial[block][j] = sum over the block's rows of dy_j * n_j
+__global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x,
+                                                          const bf16* __restrict__ scale,
+                                                          const float* __restrict__ rstd,
+                                                          const bf16* __restrict__ dres, bf16* __restrict__ dx,
+                                                          float* __restrict__ partial, int rows, int d) {
+  extern __shared__ float smem[];  // [waves][d]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  float* my = smem + (size_t)wave * d;
+  for (int j = lane; j < d; j += kWave) my[j] = 0.f;
+  for (int row = blockIdx.x * waves + wave; row < rows; row += gridDim.x * waves) {
+    const bf16* xr = x + (size_t)row * d;
+    const bf16* gr = dy + (size_t)row * d;
+    const float r = rstd[row];
+    float dot = 0.f;
+    for (int j = lane; j < d; j += kWave) {
+      float dn = (float)(bf16)((float)gr[j] * (float)scale[j]);
+      dot += dn * (float)xr[j];
+    }
+    dot = wave_sum(dot);
+    const float coef = r * r * r * dot / (float)d;
+    bf16* o = dx + (size_t)row * d;
+    for (int j = lane; j < d; j += kWave) {
+      float xv = (float)xr[j];
+      float g = (float)gr[j];
+      float dn = (float)(bf16)(g * (float)scale[j]);
+      float v = (float)(bf16)(r * dn - coef * xv);
+      if (dres) v += (float)dres[(size_t)row * d + j];
+      o[j] = (bf16)v;
+      my[j] += g * (float)(bf16)(xv * r);
+    }
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    float s = 0.f;
+    for (int w = 0; w < waves; ++w) s += smem[(size_t)w * d + j];
+    partial[(size_t)blockIdx.x * d + j] = s;
+  }
+}
+
+__global__ void column_sum_kernel(const float* __restrict__ partial, int parts, int d, float* __restrict__ out,
+                                  int accumulate) {
+  int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= d) return;
+  float s = 0.f;
+  for (int p = 0; p < parts; ++p) s += partial[(size_t)p * d + j];
+  out[j] = accumulate ? out[j] + s : s;
+}
+
+// ----------------------------------------------------------------------------
+// GELU, tanh approximation (jax.nn.gelu(approximate=True), train.py:1171)
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float tanh_fast(float u) {
+  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-inf.
+  float e = fast_exp2(2.0f * GPTRIG_LOG2E * u);
+  return 1.0f - 2.0f / (e + 1.0f);
+}
+__device__ __forceinline__ float gelu_f(float x) {
+  const float k = 0.7978845608028654f;  // sqrt(2/pi)
+  float u = k * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanh_fast(u));
+}
+__device__ __forceinline__ float gelu_grad_f(float x) {
+  const float k = 0.7978845608028654f;
+  float u = k * (x + 0.044715f * x * x * x);
+  float t = tanh_fast(u);
+  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * 0.044715f * x * x);
+}
+
+__global__ void gelu_fwd_kernel(const bf16* __restrict__ x, bf16* __restrict__ y, int64_t n) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(x + i);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (bf16)gelu_f((float)v[j]);
+    *reinterpret_cast<bf16x8*>(y + i) = o;
+  } else {
+    for (; i < n; ++i) y[i] = (bf16)gelu_f((float)x[i]);
+  }
+}
+
+__global__ void gelu_bwd_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x, bf16* __restrict__ dx,
+                                int64_t n) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(x + i);
+    bf16x8 g = *reinterpret_cast<const bf16x8*>(dy + i);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (bf16)((float)g[j] * gelu_grad_f((float)v[j]));
+    *reinterpret_cast<bf16x8*>(dx + i) = o;
+  } else {
+    for (; i < n; ++i) dx[i] = (bf16)((float)dy[i] * gelu_grad_f((float)x[i]));
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Interleaved RoPE, base 10000  (rig/nn.py:36-52)
+// Table: inv_freq = 10000^(-2i/D), angle = pos*inv_freq (fp32), cos/sin -> bf16.
+// In place on rows of a [rows, row_stride] buffer; position = row % seq; the
+// first `heads` head-sized column groups of each row are rotated.
+// ----------------------------------------------------------------------------
+__global__ void rope_table_kernel(bf16* __restrict__ cs, bf16* __restrict__ sn, int seq, int half, int head_dim) {
+  int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= seq * half) return;
+  int p = idx / half, i = idx % half;
+  float fraction = (float)(2 * i) / (float)head_dim;
+  float inv = powf(10000.0f, -fraction);
+  float angle = (float)p * inv;
+  cs[idx] = (bf16)cosf(angle);
+  sn[idx] = (bf16)sinf(angle);
+}
+
+template <bool kBackward>
+__global__ void rope_kernel(bf16* __restrict__ x, int64_t row_stride, int rows, int seq, int heads, int head_dim,
+                            const bf16* __restrict__ cs, const bf16* __restrict__ sn) {
+  const int half = head_dim / 2;
+  const int quads_per_row = heads * half / 4;  // 4 pairs (8 values) per thread
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * quads_per_row) return;
+  int row = (int)(t / quads_per_row);
+  int q = (int)(t % quads_per_row);
+  int pair0 = q * 4;  // pair index within the row's rotated region
+  int h = pair0 / half, i0 = pair0 % half;
+  int pos = row % seq;
+  bf16* p = x + (size_t)row * row_stride + (size_t)h * head_dim + 2 * i0;
+  bf16x8 v = *reinterpret_cast<bf16x8*>(p);
+  bf16x4 c4 = *reinterpret_cast<const bf16x4*>(cs + (size_t)pos * half + i0);
+  bf16x4 s4 = *reinterpret_cast<const bf16x4*>(sn + (size_t)pos * half + i0);
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float e = (float)v[2 * j], od = (float)v[2 * j + 1];
+    float c = (float)c4[j], s = (float)s4[j];
+    if (kBackward) s = -s;
+    o[2 * j] = (bf16)(e * c - od * s);
+    o[2 * j + 1] = (bf16)(e * s + od * c);
+  }
+  *reinterpret_cast<bf16x8*>(p) = o;
+}
+
+// ----------------------------------------------------------------------------
+// Embedding gather (train.py:1107) and its transpose (fp32 scatter-add).
+// ----------------------------------------------------------------------------
+__global__ void embedding_fwd_kernel(const int32_t* __restrict__ tok, const bf16* __restrict__ table,
+                                     bf16* __restrict__ out, int n, int d, int vocab) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int chunks = d / 8;
+  if (t >= (int64_t)n * chunks) return;
+  int row = (int)(t / chunks), c = (int)(t % chunks);
+  int id = tok[row];
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+  *reinterpret_cast<bf16x8*>(out + (size_t)row * d + 8 * c) =
+      *reinterpret_cast<const bf16x8*>(table + (size_t)id * d + 8 * c);
+}
+
+__global__ void embedding_bwd_kernel(const int32_t* __restrict__ tok, const bf16* __restrict__ dout,
+                                     float* __restrict__ dtable, int n, int d, int vocab) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int chunks = d / 8;
+  if (t >= (int64_t)n * chunks) return;
+  int row = (int)(t / chunks), c = (int)(t % chunks);
+  int id = tok[row];
+  if (id < 0 || id >= vocab) return;
+  bf16x8 g = *reinterpret_cast<const bf16x8*>(dout + (size_t)row * d + 8 * c);
+  float* dst = dtable + (size_t)id * d + 8 * c;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) atomicAdd(dst + j, (float)g[j]);
+}
+
+// ----------------------------------------------------------------------------
+// AdamW over a flat fp32 arena (train.py:1386-1445).  Tensors start on
+// `chunk`-element boundaries, so every chunk belongs to exactly one tensor;
+// chunk_tensor[c] names it and hparams[t] = {lr_mult, eps, decay} where
+// eps = adam_eps * eps_horizon * eps_mult and decay = wd * decay_horizon *
+// decay_mult (0 when the role is not decayed).  Also emits the block partial of
+// sum(g^2) (the pre-clip gradient norm, train.py:1387-1391) and the bf16
+// shadow of the updated parameter used by the next step's matmuls.
+// ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                    float* __restrict__ m, float* __restrict__ v,
+                                                    bf16* __restrict__ shadow,
+                                                    const int32_t* __restrict__ chunk_tensor,
+                                                    const float* __restrict__ hparams, int chunk, float lr,
+                                                    float beta1, float beta2, float bc1, float bc2,
+                                                    const float* __restrict__ clip_scale,
+                                                    float* __restrict__ sq_partial) {
+  __shared__ float red[4];
+  const int c = blockIdx.x;
+  const int t = chunk_tensor[c];
+  const float lr_t = lr * hparams[3 * t + 0];
+  const float eps = hparams[3 * t + 1];
+  const float decay = hparams[3 * t + 2];
+  const float clip = clip_scale ? *clip_scale : 1.0f;
+  const size_t base = (size_t)c * chunk;
+  float sq = 0.f;
+  for (int i = threadIdx.x * 4; i < chunk; i += blockDim.x * 4) {
+    const size_t k = base + i;
+    f32x4 gv = *reinterpret_cast<const f32x4*>(g + k);
+    f32x4 pv = *reinterpret_cast<const f32x4*>(p + k);
+    f32x4 mv = *reinterpret_cast<const f32x4*>(m + k);
+    f32x4 vv = *reinterpret_cast<const f32x4*>(v + k);
+    bf16x4 sv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float gr = gv[j];
+      sq += gr * gr;
+      float gj = gr * clip;
+      float mj = beta1 * mv[j] + (1.0f - beta1) * gj;
+      float vj = beta2 * vv[j] + (1.0f - beta2) * gj * gj;
+      float adam = (mj / bc1) / (sqrtf(vj / bc2) + eps);
+      float pj = pv[j] - lr_t * (adam + decay * pv[j]);
+      mv[j] = mj;
+      vv[j] = vj;
+      pv[j] = pj;
+      sv[j] = (bf16)pj;
+    }
+    *reinterpret_cast<f32x4*>(p + k) = pv;
+    *reinterpret_cast<f32x4*>(m + k) = mv;
+    *reinterpret_cast<f32x4*>(v + k) = vv;
+    if (shadow) *reinterpret_cast<bf16x4*>(shadow + k) = sv;
+  }
+  if (sq_partial) {
+    sq = wave_sum(sq);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = 0.f;
+      for (int w = 0; w < (int)(blockDim.x / 64); ++w) s += red[w];
+      sq_partial[c] = s;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) sq_partial_kernel(const float* __restrict__ x, int chunk,
+                                                         float* __restrict__ partial) {
+  __shared__ float red[4];
+  const size_t base = (size_t)blockIdx.x * chunk;
+  float sq = 0.f;
+  for (int i = threadIdx.x * 4; i < chunk; i += blockDim.x * 4) {
+    f32x4 gv = *reinterpret_cast<const f32x4*>(x + base + i);
+    sq += gv[0] * gv[0] + gv[1] * gv[1] + gv[2] * gv[2] + gv[3] * gv[3];
+  }
+  sq = wave_sum(sq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = sq;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int w = 0; w < (int)(blockDim.x / 64); ++w) s += red[w];
+    partial[blockIdx.x] = s;
+  }
+}
+
+// Sum the partials in fp64 (one block), write the norm, the clip scale
+// min(1, clip/(norm+1e-6)) and, when given, the history row (loss, lr, norm).
+__global__ void __launch_bounds__(256) finalize_norm_kernel(const float* __restrict__ partial, int parts,
+                                                            float grad_clip, float* __restrict__ norm_out,
+                                                            float* __restrict__ clip_out,
+                                                            const float* __restrict__ loss, float lr,
+                                                            float* __restrict__ history_row) {
+  __shared__ double red[256];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < parts; i += blockDim.x) s += (double)partial[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float norm = (float)sqrt(red[0]);
+    if (norm_out) *norm_out = norm;
+    if (clip_out) *clip_out = grad_clip > 0.f ? fminf(1.0f, grad_clip / (norm + 1.0e-6f)) : 1.0f;
+    if (history_row) {
+      history_row[0] = loss ? *loss : 0.f;
+      history_row[1] = lr;
+      history_row[2] = norm;
+    }
+  }
+}
+
+__global__ void cast_f32_bf16_kernel(const float* __restrict__ x, bf16* __restrict__ y, int64_t n) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 4 <= n) {
+    f32x4 v = *reinterpret_cast<const f32x4*>(x + i);
+    bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+    *reinterpret_cast<bf16x4*>(y + i) = o;
+  } else {
+    for (; i < n; ++i) y[i] = (bf16)x[i];
+  }
+}
+
+// out += weight * sum(x)  (fp32 atomics, one per block)
+__global__ void __launch_bounds__(256) weighted_sum_kernel(const float* __restrict__ x, int64_t n, float weight,
+                                                           float* __restrict__ out) {
+  __shared__ float red[4];
+  float s = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    s += x[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicAdd(out, weight * (red[0] + red[1] + red[2] + red[3]));
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ x, int64_t n, float value) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = value;
+}
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, int rows, int d, void* stream) {
+  if (!x || !scale || !y) return GPTRIG_E_NULL;
+  if (rows < 0 || d <= 0) return GPTRIG_E_SHAPE;
+  if (rows == 0) return GPTRIG_OK;
+  dim3 block(256);
+  dim3 grid(ceil_div(rows, 4));
+  rmsnorm_fwd_kernel<<<grid, block, 0, (hipStream_t)stream>>>((const bf16*)x, (const bf16*)scale, (bf16*)y, rstd,
+                                                               rows, d);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d) {
+  int blocks = rows < 4 ? 1 : (ceil_div(rows, 4) < 1024 ? ceil_div(rows, 4) : 1024);
+  return (size_t)blocks * d * sizeof(float);
+}
+
+int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const float* rstd, const void* dresidual,
+                       void* dx, float* dscale, int accumulate_dscale, void* workspace, size_t workspace_bytes,
+                       int rows, int d, void* stream) {
+  if (!dy || !x || !scale || !rstd || !dx || !dscale || !workspace) return GPTRIG_E_NULL;
+  if (rows <= 0 || d <= 0) return GPTRIG_E_SHAPE;
+  if ((size_t)d * 4 * sizeof(float) > 64 * 1024) return GPTRIG_E_UNSUPPORTED;
+  if (workspace_bytes < gptrig_rmsnorm_bwd_workspace_bytes(rows, d)) return GPTRIG_E_WORKSPACE;
+  int blocks = rows < 4 ? 1 : (ceil_div(rows, 4) < 1024 ? ceil_div(rows, 4) : 1024);
+  hipStream_t s = (hipStream_t)stream;
+  rmsnorm_bwd_kernel<<<blocks, 256, 4 * d * sizeof(float), s>>>((const bf16*)dy, (const bf16*)x, (const bf16*)scale,
+                                                                  rstd, (const bf16*)dresidual, (bf16*)dx,
+                                                                  (float*)workspace, rows, d);
+  GPTRIG_CHECK_LAUNCH();
+  column_sum_kernel<<<ceil_div(d, 256), 256, 0, s>>>((const float*)workspace, blocks, d, dscale, accumulate_dscale);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_gelu_fwd(const void* x, void* y, int64_t n, void* stream) {
+  if (!x || !y) return GPTRIG_E_NULL;
+  if (n < 0) return GPTRIG_E_SHAPE;
+  if (n == 0) return GPTRIG_OK;
+  gelu_fwd_kernel<<<ceil_div(ceil_div(n, 8), 256), 256, 0, (hipStream_t)stream>>>((const bf16*)x, (bf16*)y, n);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_gelu_bwd(const void* dy, const void* x, void* dx, int64_t n, void* stream) {
+  if (!dy || !x || !dx) return GPTRIG_E_NULL;
+  if (n < 0) return GPTRIG_E_SHAPE;
+  if (n == 0) return GPTRIG_OK;
+  gelu_bwd_kernel<<<ceil_div(ceil_div(n, 8), 256), 256, 0, (hipStream_t)stream>>>((const bf16*)dy, (const bf16*)x,
+                                                                                   (bf16*)dx, n);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_rope_table(void* cos_table, void* sin_table, int seq, int head_dim, void* stream) {
+  if (!cos_table || !sin_table) return GPTRIG_E_NULL;
+  if (seq <= 0 || head_dim <= 0 || (head_dim & 1)) return GPTRIG_E_SHAPE;
+  int half = head_dim / 2;
+  rope_table_kernel<<<ceil_div((long long)seq * half, 256), 256, 0, (hipStream_t)stream>>>(
+      (bf16*)cos_table, (bf16*)sin_table, seq, half, head_dim);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+static int rope_launch(bool backward, void* x, int64_t row_stride, int rows, int seq, int heads, int head_dim,
+                       const void* cs, const void* sn, void* stream) {
+  if (!x || !cs || !sn) return GPTRIG_E_NULL;
+  if (rows < 0 || seq <= 0 || heads <= 0 || head_dim <= 0) return GPTRIG_E_SHAPE;
+  if (head_dim % 8 || row_stride % 8 || row_stride < (int64_t)heads * head_dim) return GPTRIG_E_SHAPE;
+  if (rows == 0) return GPTRIG_OK;
+  long long threads = (long long)rows * heads * (head_dim / 2) / 4;
+  if (backward)
+    rope_kernel<true><<<ceil_div(threads, 256), 256, 0, (hipStream_t)stream>>>(
+        (bf16*)x, row_stride, rows, seq, heads, head_dim, (const bf16*)cs, (const bf16*)sn);
+  else
+    rope_kernel<false><<<ceil_div(threads, 256), 256, 0, (hipStream_t)stream>>>(
+        (bf16*)x, row_stride, rows, seq, heads, head_dim, (const bf16*)cs, (const bf16*)sn);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_rope_fwd(void* x, int64_t row_stride, int rows, int seq, int heads, int head_dim, const void* cos_table,
+                    const void* sin_table, void* stream) {
+  return rope_launch(false, x, row_stride, rows, seq, heads, head_dim, cos_table, sin_table, stream);
+}
+
+int gptrig_rope_bwd(void* dx, int64_t row_stride, int rows, int seq, int heads, int head_dim,
+                    const void* cos_table, const void* sin_table, void* stream) {
+  return rope_launch(true, dx, row_stride, rows, seq, heads, head_dim, cos_table, sin_table, stream);
+}
+
+int gptrig_embedding_fwd(const int32_t* tokens, const void* table, void* out, int n, int d, int vocab,
+                         void* stream) {
+  if (!tokens || !table || !out) return GPTRIG_E_NULL;
+  if (n < 0 || d <= 0 || d % 8 || vocab <= 0) return GPTRIG_E_SHAPE;
+  if (n == 0) return GPTRIG_OK;
+  embedding_fwd_kernel<<<ceil_div((long long)n * (d / 8), 256), 256, 0, (hipStream_t)stream>>>(
+      tokens, (const bf16*)table, (bf16*)out, n, d, vocab);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_embedding_bwd(const int32_t* tokens, const void* dout, float* dtable, int n, int d, int vocab,
+                         void* stream) {
+  if (!tokens || !dout || !dtable) return GPTRIG_E_NULL;
+  if (n < 0 || d <= 0 || d % 8 || vocab <= 0) return GPTRIG_E_SHAPE;
+  if (n == 0) return GPTRIG_OK;
+  embedding_bwd_kernel<<<ceil_div((long long)n * (d / 8), 256), 256, 0, (hipStream_t)stream>>>(
+      tokens, (const bf16*)dout, dtable, n, d, vocab);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_adamw(float* param, const float* grad, float* m, float* v, void* param_bf16, const int32_t* chunk_tensor,
+                 const float* tensor_hparams, int64_t n_chunks, int chunk, float lr, float beta1, float beta2,
+                 int step, const float* clip_scale, float* sq_partials, void* stream) {
+  if (!param || !grad || !m || !v || !chunk_tensor || !tensor_hparams) return GPTRIG_E_NULL;
+  if (n_chunks < 0 || chunk <= 0 || chunk % 1024 || step <= 0) return GPTRIG_E_SHAPE;
+  if (n_chunks == 0) return GPTRIG_OK;
+  // The reference divides by float32 bias corrections 1 - beta^step.
+  float bc1 = 1.0f - powf(beta1, (float)step);
+  float bc2 = 1.0f - powf(beta2, (float)step);
+  adamw_kernel<<<(unsigned)n_chunks, 256, 0, (hipStream_t)stream>>>(param, grad, m, v, (bf16*)param_bf16,
+                                                                      chunk_tensor, tensor_hparams, chunk, lr, beta1,
+                                                                      beta2, bc1, bc2, clip_scale,
+                                                                      sq_partials);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_sq_norm_partials(const float* x, int64_t n_chunks, int chunk, float* partials, void* stream) {
+  if (!x || !partials) return GPTRIG_E_NULL;
+  if (n_chunks < 0 || chunk <= 0 || chunk % 1024) return GPTRIG_E_SHAPE;
+  if (n_chunks == 0) return GPTRIG_OK;
+  sq_partial_kernel<<<(unsigned)n_chunks, 256, 0, (hipStream_t)stream>>>(x, chunk, partials);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_finalize_norm(const float* partials, int parts, float grad_clip, float* norm_out, float* clip_out,
+                         const float* loss, float lr, float* history_row, void* stream) {
+  if (!partials) return GPTRIG_E_NULL;
+  if (parts <= 0) return GPTRIG_E_SHAPE;
+  finalize_norm_kernel<<<1, 256, 0, (hipStream_t)stream>>>(partials, parts, grad_clip, norm_out, clip_out, loss, lr,
+                                                          history_row);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream) {
+  if (!x || !y) return GPTRIG_E_NULL;
+  if (n < 0) return GPTRIG_E_SHAPE;
+  if (n == 0) return GPTRIG_OK;
+  cast_f32_bf16_kernel<<<ceil_div(ceil_div(n, 4), 256), 256, 0, (hipStream_t)stream>>>(x, (bf16*)y, n);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_weighted_sum(const float* x, int64_t n, float weight, float* out, void* stream) {
+  if (!x || !out) return GPTRIG_E_NULL;
+  if (n <= 0) return GPTRIG_E_SHAPE;
+  int blocks = ceil_div(n, 256);
+  if (blocks > 1024) blocks = 1024;
+  weighted_sum_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(x, n, weight, out);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_fill_f32(float* x, int64_t n, float value, void* stream) {
+  if (!x) return GPTRIG_E_NULL;
+  if (n < 0) return GPTRIG_E_SHAPE;
+  if (n == 0) return GPTRIG_OK;
+  fill_f32_kernel<<<ceil_div(n, 256), 256, 0, (hipStream_t)stream>>>(x, n, value);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,373 @@
+"""The GPT training step on one MI355X, composed from the gfx950 kernels.
+
+Restates ``recipes/reference/train.py``: ``init_params`` (``:865-901``),
+``gpt_hidden`` (``:1096-1176``), ``cross_entropy`` with the tiled loss
+(``:1194-1210``) and ``_apply_training_update`` (``:1362-1457``).
+
+Memory layout (HBM):
+* one float32 arena holds every parameter, each tensor starting on a
+  4096-element chunk boundary, plus same-shaped float32 arenas for the
+  gradient and the two Adam moments;
+* a bfloat16 shadow arena holds ``bf16(param)``, refreshed by the AdamW kernel,
+  which is exactly the reference's ``W.astype(bfloat16)`` at use;
+* activations are ``[tokens, features]`` bf16 row-major; attention reads
+  q/k/v in place from the ``[tokens, 3*d_model]`` projection (BHSD strides)
+  and writes its output as ``[tokens, d_model]``.
+
+The forward and backward passes are explicit (no autograd tape): RMSNorm,
+RoPE, attention, GELU, the LM-head cross-entropy, the embedding scatter and
+AdamW are HIP kernels; the dense projections are hipBLASLt GEMMs through
+torch.  Weight gradients accumulate in float32 across micro-batches; the
+global batch is split into equal micro-batches whose mean losses are averaged,
+which equals the reference's single-batch token mean.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib
+from .attention import attention_softmax_scale, document_segments
+from .kernels import linear_cross_entropy as lce
+from .nn import normal, rmsnorm_backward, rmsnorm_forward, rope_inplace
+from .optim import OptimizerConfig, effective_adam_betas, learning_rate, tensor_hparams
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+CHUNK = 4096
+BLOCK_LEAVES = ("ln1_scale", "qkv_w", "qkv_b", "attn_w", "attn_b",
+                "ln2_scale", "mlp_up_w", "mlp_up_b", "mlp_down_w", "mlp_down_b")
+
+
+@dataclass(frozen=True)
+class GPTConfig:
+    """Model/optimizer fields of the reference ``Config`` (``train.py:176-282``)."""
+
+    layers: int = 12
+    heads: int = 12
+    d_model: int = 768
+    mlp_mult: int = 4
+    vocab_size: int = 50304
+    semantic_vocab_size: int = 50304
+    seq_len: int = 1024
+    batch_size: int = 128
+    micro_batch_size: int = 32
+    parameterization: str = "standard"
+    base_width: int = 768
+    base_depth: int = 12
+    depth_alpha: float = 0.0
+    init_std: float = 0.02
+    attention_scale: str = "inverse_sqrt_head_dim"
+    embeddings: str = "untied"
+    vocab_tile_size: int = 2048
+    document_masking: bool = False
+    document_boundary_token: int = 50256
+    optimizer: OptimizerConfig = field(default_factory=OptimizerConfig)
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.heads
+
+    @property
+    def width_multiplier(self) -> float:
+        return self.d_model / float(self.base_width)
+
+    @property
+    def depth_multiplier(self) -> float:
+        return self.layers / float(self.base_depth)
+
+    def validate(self) -> None:
+        if self.d_model % self.heads:
+            raise ValueError("d_model must be divisible by heads")
+        if self.head_dim % 2:
+            raise ValueError("head dimension must be even for RoPE")
+        if self.semantic_vocab_size > self.vocab_size:
+            raise ValueError("semantic_vocab_size must not exceed vocab_size")
+        if self.batch_size % self.micro_batch_size:
+            raise ValueError("micro_batch_size must divide batch_size")
+        if self.head_dim not in (64, 128) or self.d_model % 64:
+            raise ValueError("the HIP step needs head_dim in {64, 128} and d_model % 64 == 0")
+
+
+def init_params(config: GPTConfig, seed: int) -> dict[str, np.ndarray]:
+    """``init_params`` (``train.py:865-901``) as a flat ``{path: float32}``
+    mapping in the reference's draw order (numpy PCG64, so bit-identical)."""
+
+    rng = np.random.default_rng(seed)
+    d = config.d_model
+    hidden = config.mlp_mult * d
+    hidden_scale = (config.init_std / math.sqrt(config.width_multiplier)
+                    if config.parameterization == "completep_fixed_tpp_v1" else 0.02)
+    flat: dict[str, np.ndarray] = {}
+    blocks = []
+    for _ in range(config.layers):
+        blocks.append({
+            "ln1_scale": np.ones((d,), np.float32),
+            "qkv_w": normal(rng, (d, 3 * d), hidden_scale),
+            "qkv_b": np.zeros((3 * d,), np.float32),
+            "attn_w": normal(rng, (d, d), hidden_scale),
+            "attn_b": np.zeros((d,), np.float32),
+            "ln2_scale": np.ones((d,), np.float32),
+            "mlp_up_w": normal(rng, (d, hidden), hidden_scale),
+            "mlp_up_b": np.zeros((hidden,), np.float32),
+            "mlp_down_w": normal(rng, (hidden, d), hidden_scale),
+            "mlp_down_b": np.zeros((d,), np.float32),
+        })
+    flat["token_embedding"] = normal(rng, (config.vocab_size, d), config.init_std)
+    for i, block in enumerate(blocks):
+        for name in BLOCK_LEAVES:
+            flat[f"blocks/{i}/{name}"] = block[name]
+    flat["final_ln_scale"] = np.ones((d,), np.float32)
+    if config.embeddings == "untied":
+        flat["output_embedding"] = normal(rng, (config.vocab_size, d), config.init_std / config.width_multiplier)
+    return flat
+
+
+class ParamArena:
+    """Flat float32 parameter / gradient / moment arenas and the bf16 shadow."""
+
+    def __init__(self, flat: dict[str, np.ndarray], device):
+        self.paths = list(flat)
+        self.shapes = {k: tuple(v.shape) for k, v in flat.items()}
+        self.offsets: dict[str, int] = {}
+        off = 0
+        for k, v in flat.items():
+            self.offsets[k] = off
+            off += (v.size + CHUNK - 1) // CHUNK * CHUNK
+        self.total = off
+        self.n_chunks = off // CHUNK
+        host = torch.zeros(off, dtype=F32)
+        chunk_tensor = np.zeros(self.n_chunks, np.int32)
+        for i, (k, v) in enumerate(flat.items()):
+            o = self.offsets[k]
+            host[o:o + v.size] = torch.from_numpy(np.ascontiguousarray(v).reshape(-1))
+            chunk_tensor[o // CHUNK:(o + v.size + CHUNK - 1) // CHUNK] = i
+        self.p = host.to(device)
+        self.g = torch.zeros(off, dtype=F32, device=device)
+        self.m = torch.zeros(off, dtype=F32, device=device)
+        self.v = torch.zeros(off, dtype=F32, device=device)
+        self.shadow = torch.empty(off, dtype=BF16, device=device)
+        _lib.call("gptrig_cast_f32_bf16", self.p.data_ptr(), self.shadow.data_ptr(), off, _lib.stream())
+        self.chunk_tensor = torch.from_numpy(chunk_tensor).to(device)
+
+    def _view(self, arena: torch.Tensor, path: str) -> torch.Tensor:
+        o = self.offsets[path]
+        shape = self.shapes[path]
+        return arena[o:o + int(np.prod(shape))].view(shape)
+
+    def param(self, path):
+        return self._view(self.p, path)
+
+    def grad(self, path):
+        return self._view(self.g, path)
+
+    def w(self, path):
+        """bf16 shadow (``param.astype(bfloat16)``)."""
+        return self._view(self.shadow, path)
+
+    def numel(self) -> int:
+        return sum(int(np.prod(s)) for s in self.shapes.values())
+
+
+class GPTTrainer:
+    """One-GPU training step for the reference GPT (``train_step``, ``train.py:1460-1472``)."""
+
+    def __init__(self, config: GPTConfig, seed: int = 0, device: str = "cuda:0", history_steps: int | None = None):
+        config.validate()
+        self.config = config
+        self.device = torch.device(device)
+        self.arena = ParamArena(init_params(config, seed), self.device)
+        self.step_count = 0
+        self.beta1, self.beta2 = effective_adam_betas(config.optimizer)
+        self.hparams = torch.from_numpy(
+            tensor_hparams(self.arena.paths, config.optimizer, config.parameterization, config.width_multiplier,
+                           config.depth_multiplier, config.depth_alpha)).to(self.device)
+        steps = history_steps or config.optimizer.steps
+        self.history = torch.zeros((steps, 3), dtype=F32, device=self.device)
+        self.loss = torch.zeros(1, dtype=F32, device=self.device)
+        self.sq_partials = torch.zeros(self.arena.n_chunks, dtype=F32, device=self.device)
+        self.norm = torch.zeros(1, dtype=F32, device=self.device)
+        self.clip = torch.ones(1, dtype=F32, device=self.device)
+        self.head_path = "output_embedding" if config.embeddings == "untied" else "token_embedding"
+        self.scale = attention_softmax_scale(config.attention_scale, config.head_dim)
+        self.residual_scale = config.depth_multiplier ** (-config.depth_alpha)
+        self._ws: dict[str, torch.Tensor] = {}
+        self.timers = None  # optional {name: list[(start_event, end_event)]}
+
+    # -- helpers -----------------------------------------------------------------
+    def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
+        ws = self._ws.get(name)
+        if ws is None or ws.numel() < nbytes:
+            ws = _lib.workspace(nbytes, self.device)
+            self._ws[name] = ws
+        return ws
+
+    def _timed(self, name):
+        timers = self.timers
+
+        class _Ctx:
+            def __enter__(self_inner):
+                if timers is not None:
+                    self_inner.s = torch.cuda.Event(enable_timing=True)
+                    self_inner.e = torch.cuda.Event(enable_timing=True)
+                    self_inner.s.record()
+
+            def __exit__(self_inner, *exc):
+                if timers is not None:
+                    self_inner.e.record()
+                    timers.setdefault(name, []).append((self_inner.s, self_inner.e))
+
+        return _Ctx()
+
+    def _residual(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        if self.residual_scale == 1.0:
+            return x + out
+        return x + (out * self.residual_scale).to(BF16)
+
+    # -- forward / backward of one micro-batch --------------------------------------
+    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float) -> None:
+        c = self.config
+        A = self.arena
+        Bm, S = tokens.shape
+        N, d, H, D = Bm * S, c.d_model, c.heads, c.head_dim
+        stream = _lib.stream()
+        tok = tokens.reshape(-1).to(torch.int32).contiguous()
+        tgt = targets.reshape(-1).to(torch.int32).contiguous()
+        seg = document_segments(tokens, c.document_boundary_token).contiguous() if c.document_masking else None
+
+        x = torch.empty((N, d), dtype=BF16, device=self.device)
+        _lib.call("gptrig_embedding_fwd", tok.data_ptr(), A.w("token_embedding").data_ptr(), x.data_ptr(), N, d,
+                  c.vocab_size, stream)
+        # strides (elements) of q/k/v inside the [N, 3d] projection, of o/do in [N, d]
+        st_qkv = (S * 3 * d, D, 3 * d)
+        st_o = (S * d, D, d)
+        attn_strides = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o], dtype=torch.int64)
+        bwd_strides = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o, *st_o, *st_qkv, *st_qkv, *st_qkv],
+                                   dtype=torch.int64)
+        saved = []
+        for i in range(c.layers):
+            p = f"blocks/{i}/"
+            xn1, rstd1 = rmsnorm_forward(x, A.w(p + "ln1_scale"))
+            qkv = torch.addmm(A.w(p + "qkv_b"), xn1, A.w(p + "qkv_w"))
+            rope_inplace(qkv, 3 * d, N, S, 2 * H, D)
+            o = torch.empty((N, d), dtype=BF16, device=self.device)
+            lse = torch.empty((Bm, H, S), dtype=F32, device=self.device)
+            with self._timed("attn_fwd"):
+                _lib.call("gptrig_attn_fwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
+                          _lib.ptr(seg), o.data_ptr(), lse.data_ptr(), Bm, H, S, D, attn_strides.data_ptr(),
+                          self.scale, stream)
+            x1 = self._residual(x, torch.addmm(A.w(p + "attn_b"), o, A.w(p + "attn_w")))
+            xn2, rstd2 = rmsnorm_forward(x1, A.w(p + "ln2_scale"))
+            h = torch.addmm(A.w(p + "mlp_up_b"), xn2, A.w(p + "mlp_up_w"))
+            g = torch.empty_like(h)
+            _lib.call("gptrig_gelu_fwd", h.data_ptr(), g.data_ptr(), h.numel(), stream)
+            x2 = self._residual(x1, torch.addmm(A.w(p + "mlp_down_b"), g, A.w(p + "mlp_down_w")))
+            saved.append((x, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g))
+            x = x2
+        xf, rstdf = rmsnorm_forward(x, A.w("final_ln_scale"))
+        head = A.w(self.head_path)
+        losses = torch.empty(N, dtype=F32, device=self.device)
+        lse_ce = torch.empty(N, dtype=F32, device=self.device)
+        ws = self._workspace("flce_fwd", _lib.query("gptrig_flce_fwd_workspace_bytes", N, d, c.vocab_size))
+        with self._timed("flce"):
+            _lib.call("gptrig_flce_fwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
+                      lse_ce.data_ptr(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size,
+                      stream)
+        _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
+
+        # ---- backward ----
+        chunk = lce.chunk_for(c.vocab_tile_size if c.vocab_tile_size > 2048 else 4096)
+        ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
+        dxf = torch.empty((N, d), dtype=BF16, device=self.device)
+        with self._timed("flce"):
+            _lib.call("gptrig_flce_bwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(), None,
+                      loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, ws.data_ptr(), ws.numel(),
+                      N, d, c.vocab_size, c.semantic_vocab_size, chunk, stream)
+        dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True)
+        attn_ws = self._workspace("attn_bwd", _lib.query("gptrig_attn_bwd_workspace_bytes", Bm, H, S, D))
+        for i in reversed(range(c.layers)):
+            p = f"blocks/{i}/"
+            x_in, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g = saved.pop()
+            dm = dx if self.residual_scale == 1.0 else (dx * self.residual_scale).to(BF16)
+            self._weight_grad(p + "mlp_down", g, dm)
+            dg = torch.mm(dm, A.w(p + "mlp_down_w").t())
+            dh = torch.empty_like(dg)
+            _lib.call("gptrig_gelu_bwd", dg.data_ptr(), h.data_ptr(), dh.data_ptr(), dh.numel(), stream)
+            self._weight_grad(p + "mlp_up", xn2, dh)
+            dxn2 = torch.mm(dh, A.w(p + "mlp_up_w").t())
+            dx1, _ = rmsnorm_backward(dxn2, x1, A.w(p + "ln2_scale"), rstd2, A.grad(p + "ln2_scale"), True,
+                                      dresidual=dx)
+            da = dx1 if self.residual_scale == 1.0 else (dx1 * self.residual_scale).to(BF16)
+            self._weight_grad(p + "attn", o, da)
+            do = torch.mm(da, A.w(p + "attn_w").t())
+            dqkv = torch.empty((N, 3 * d), dtype=BF16, device=self.device)
+            with self._timed("attn_bwd"):
+                _lib.call("gptrig_attn_bwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
+                          o.data_ptr(), do.data_ptr(), lse.data_ptr(), _lib.ptr(seg), dqkv.data_ptr(),
+                          dqkv[:, d:].data_ptr(), dqkv[:, 2 * d:].data_ptr(), attn_ws.data_ptr(), attn_ws.numel(),
+                          Bm, H, S, D, bwd_strides.data_ptr(), self.scale, stream)
+            rope_inplace(dqkv, 3 * d, N, S, 2 * H, D, backward=True)
+            self._weight_grad(p + "qkv", xn1, dqkv)
+            dxn1 = torch.mm(dqkv, A.w(p + "qkv_w").t())
+            dx, _ = rmsnorm_backward(dxn1, x_in, A.w(p + "ln1_scale"), rstd1, A.grad(p + "ln1_scale"), True,
+                                     dresidual=dx1)
+        _lib.call("gptrig_embedding_bwd", tok.data_ptr(), dx.data_ptr(), A.grad("token_embedding").data_ptr(), N, d,
+                  c.vocab_size, stream)
+
+    def _weight_grad(self, prefix: str, inp: torch.Tensor, dout: torch.Tensor) -> None:
+        """dW += inp^T dout and db += sum_rows(dout), both float32."""
+
+        A = self.arena
+        gw = A.grad(prefix + "_w")
+        # hipBLASLt: bf16 operands, float32 accumulator read and written in place.
+        torch.addmm(gw, inp.t(), dout, out_dtype=F32, out=gw)
+        gb = A.grad(prefix + "_b")
+        gb.add_(dout.sum(0, dtype=F32))
+
+    # -- the step ----------------------------------------------------------------------
+    def train_step(self, x: torch.Tensor, y: torch.Tensor) -> None:
+        """One optimizer step on a global batch ``x, y`` (int32 ``[batch, seq]``).
+
+        Everything stays on the device; ``history`` row ``step-1`` receives
+        ``(loss, lr, grad_norm)`` (``train.py:1446-1447``).
+        """
+
+        c = self.config
+        A = self.arena
+        stream = _lib.stream()
+        A.g.zero_()
+        self.loss.zero_()
+        mb = c.micro_batch_size
+        n_micro = x.shape[0] // mb
+        weight = 1.0 / (n_micro * mb * x.shape[1])
+        for j in range(n_micro):
+            self._forward_backward(x[j * mb:(j + 1) * mb], y[j * mb:(j + 1) * mb], weight)
+        self.step_count += 1
+        step = self.step_count
+        lr = learning_rate(step, c.optimizer)
+        row = self.history[step - 1] if step <= self.history.shape[0] else None
+        with self._timed("adamw"):
+            if c.optimizer.grad_clip > 0.0:
+                _lib.call("gptrig_sq_norm_partials", A.g.data_ptr(), A.n_chunks, CHUNK, self.sq_partials.data_ptr(),
+                          stream)
+                _lib.call("gptrig_finalize_norm", self.sq_partials.data_ptr(), A.n_chunks, c.optimizer.grad_clip,
+                          self.norm.data_ptr(), self.clip.data_ptr(), self.loss.data_ptr(), lr,
+                          _lib.ptr(row), stream)
+                _lib.call("gptrig_adamw", A.p.data_ptr(), A.g.data_ptr(), A.m.data_ptr(), A.v.data_ptr(),
+                          A.shadow.data_ptr(), A.chunk_tensor.data_ptr(), self.hparams.data_ptr(), A.n_chunks, CHUNK,
+                          lr, self.beta1, self.beta2, step, self.clip.data_ptr(), None, stream)
+            else:
+                _lib.call("gptrig_adamw", A.p.data_ptr(), A.g.data_ptr(), A.m.data_ptr(), A.v.data_ptr(),
+                          A.shadow.data_ptr(), A.chunk_tensor.data_ptr(), self.hparams.data_ptr(), A.n_chunks, CHUNK,
+                          lr, self.beta1, self.beta2, step, None, self.sq_partials.data_ptr(), stream)
+                _lib.call("gptrig_finalize_norm", self.sq_partials.data_ptr(), A.n_chunks, 0.0, self.norm.data_ptr(),
+                          None, self.loss.data_ptr(), lr, _lib.ptr(row), stream)
+
+    def history_rows(self) -> np.ndarray:
+        """Copy the on-device ``(loss, lr, grad_norm)`` history (one sync)."""
+
+        return self.history[: self.step_count].cpu().numpy()

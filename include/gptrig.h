@@ -1,0 +1,175 @@
+/*
+ * gptrig: C ABI of the MI355X (gfx950) training-step hot path of the GPT
+ * speedrun rig (honglu2875/GPT-speedrun-TPU).
+ *
+ * Conventions (every entry point):
+ *   - returns GPTRIG_OK (0) or a negative GPTRIG_E_* status; nothing throws;
+ *   - validation happens on the host before any launch (bad shape, null
+ *     pointer, unsupported head_dim ...), mirroring the reference's
+ *     ValueError/TypeError-before-compilation contract;
+ *   - the caller owns every buffer (inputs, outputs, workspace); nothing here
+ *     allocates, frees or synchronises the host;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = the null stream);
+ *   - "bf16" buffers hold bfloat16, "f32" float32, "i32" int32.
+ *
+ * Each entry point maps 1:1 onto an XLA-FFI custom-call handler (buffers,
+ * stream, scalar attributes); see INTEGRATION.md for the reference-side
+ * binding.
+ */
+#ifndef GPTRIG_H_
+#define GPTRIG_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPTRIG_OK 0
+#define GPTRIG_E_NULL (-1)        /* a required pointer is NULL */
+#define GPTRIG_E_SHAPE (-2)       /* sizes/strides violate the contract */
+#define GPTRIG_E_DTYPE (-3)       /* unsupported element type */
+#define GPTRIG_E_UNSUPPORTED (-4) /* legal but not implemented (e.g. head_dim) */
+#define GPTRIG_E_LAUNCH (-5)      /* the HIP launch failed */
+#define GPTRIG_E_WORKSPACE (-6)   /* workspace smaller than the query says */
+
+/* Library identity and status text. */
+const char* gptrig_version(void);
+const char* gptrig_status_string(int status);
+
+/* ------------------------------------------------------------------------
+ * Causal flash attention.
+ * Replaces the Pallas kernels of rig/kernels/tpu_flash_attention.py:
+ *   forward  _tpu_flash_forward            (:351-476, kernel :236-348)
+ *   backward _tpu_flash_backward           (:704-904, kernels :479-701)
+ * Tensors are logical BHSD [batch, heads, seq, head_dim] bf16 with head_dim
+ * contiguous.  `strides` (nullable) gives element strides (batch, head, seq)
+ * per tensor, 3 int64 each, in the order the tensors appear in the argument
+ * list; NULL means contiguous BHSD for all.  head_dim in {64, 128}; any
+ * seq >= 1 (keys at or past `seq` never exist, so right-padding is implicit).
+ * segment_ids (nullable) is i32 [batch, seq]: positions attend only within
+ * their own id (document masking, :312-318).  lse is f32 [batch, heads, seq],
+ * natural log: log(sum_j exp(scale*q.k_j)).
+ * ---------------------------------------------------------------------- */
+int gptrig_attn_fwd(const void* q, const void* k, const void* v, const int32_t* segment_ids, void* o, float* lse,
+                    int batch, int heads, int seq, int head_dim, const int64_t* strides /* q,k,v,o */,
+                    float softmax_scale, void* stream);
+
+/* Workspace of gptrig_attn_bwd: Delta (f32 [B,H,S]) and the f32 dQ accumulator. */
+size_t gptrig_attn_bwd_workspace_bytes(int batch, int heads, int seq, int head_dim);
+
+/* dQ, dK, dV (bf16) from q, k, v, o, dO (bf16) and the forward's lse. */
+int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                    const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace,
+                    size_t workspace_bytes, int batch, int heads, int seq, int head_dim,
+                    const int64_t* strides /* q,k,v,o,dout,dq,dk,dv */, float softmax_scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused linear cross-entropy (LM head + online log-sum-exp + loss + dh/dW).
+ * Replaces rig/kernels/linear_cross_entropy.py:
+ *   forward  _losses_and_residual   (:115-179)
+ *   backward _tiled_losses_bwd      (:220-302)
+ * hidden bf16 [n, d] (d % 64 == 0), weight bf16 [vocab, d] (the compute-dtype
+ * copy of the embedding), targets i32 [n].  Rows at or past `semantic_vocab`
+ * get no probability mass and exactly zero weight gradient; a target outside
+ * [0, semantic_vocab) gives loss +inf and contributes no gradient.
+ * ---------------------------------------------------------------------- */
+size_t gptrig_flce_fwd_workspace_bytes(int n, int d, int vocab);
+int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
+                    void* workspace, size_t workspace_bytes, int n, int d, int vocab, int semantic_vocab,
+                    void* stream);
+
+/* Backward.  cotangent: f32 [n] per-token loss cotangents, or NULL to use the
+ * scalar `cotangent_scale` for every token (1/n for the mean loss).
+ * dhidden: bf16 [n, d].  dweight: f32 [vocab, d]; accumulate_dweight != 0 adds
+ * into it (micro-batch accumulation), otherwise it is overwritten.
+ * vocab_chunk (multiple of 256, 0 = default) bounds the [n, vocab_chunk]
+ * logit-gradient workspace. */
+size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk);
+int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
+                    const float* cotangent, float cotangent_scale, void* dhidden, float* dweight,
+                    int accumulate_dweight, void* workspace, size_t workspace_bytes, int n, int d, int vocab,
+                    int semantic_vocab, int vocab_chunk, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm, rig/nn.py:26-33 (rms_norm): y = bf16(bf16(x*rsqrt(mean(x^2)+1e-5)) * scale).
+ * x, y bf16 [rows, d]; scale bf16 [d]; rstd f32 [rows] (saved for backward).
+ * ---------------------------------------------------------------------- */
+int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, int rows, int d, void* stream);
+size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d);
+/* dx bf16 = d rms_norm/dx (+ dresidual if non-NULL); dscale f32 [d] (+= if accumulate). */
+int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const float* rstd, const void* dresidual,
+                       void* dx, float* dscale, int accumulate_dscale, void* workspace, size_t workspace_bytes,
+                       int rows, int d, void* stream);
+
+/* GELU, tanh approximation: jax.nn.gelu(approximate=True) at
+ * recipes/reference/train.py:1171.  bf16 [n]. */
+int gptrig_gelu_fwd(const void* x, void* y, int64_t n, void* stream);
+int gptrig_gelu_bwd(const void* dy, const void* x, void* dx, int64_t n, void* stream);
+
+/* Interleaved RoPE, base 10000: rig/nn.py:36-52 (apply_rotary).
+ * rope_table fills bf16 cos/sin [seq, head_dim/2].  rope_fwd/bwd rotate, in
+ * place, the first `heads` head_dim-wide column groups of each row of a bf16
+ * [rows, row_stride] buffer; the position of a row is row % seq. */
+int gptrig_rope_table(void* cos_table, void* sin_table, int seq, int head_dim, void* stream);
+int gptrig_rope_fwd(void* x, int64_t row_stride, int rows, int seq, int heads, int head_dim, const void* cos_table,
+                    const void* sin_table, void* stream);
+int gptrig_rope_bwd(void* dx, int64_t row_stride, int rows, int seq, int heads, int head_dim,
+                    const void* cos_table, const void* sin_table, void* stream);
+
+/* Token-embedding gather (recipes/reference/train.py:1107) and its transpose:
+ * out bf16 [n, d] = table[tokens]; dtable f32 [vocab, d] += scatter(dout). */
+int gptrig_embedding_fwd(const int32_t* tokens, const void* table, void* out, int n, int d, int vocab,
+                         void* stream);
+int gptrig_embedding_bwd(const int32_t* tokens, const void* dout, float* dtable, int n, int d, int vocab,
+                         void* stream);
+
+/* ------------------------------------------------------------------------
+ * AdamW over one flat f32 arena: recipes/reference/train.py:1386-1445
+ * (_apply_training_update), with the per-tensor multipliers of
+ * optimizer_hyperparameter_trees (:1274-1333) and the decay mask of
+ * weight_decay_mask (:1252-1271) folded into tensor_hparams[t] =
+ * {lr_mult, epsilon, decay}.  Every tensor starts on a `chunk` boundary
+ * (chunk % 1024 == 0) and chunk_tensor[c] names chunk c's tensor.
+ * param_bf16 (nullable) receives bf16(updated param).  clip_scale (nullable
+ * device scalar) multiplies the gradient.  sq_partials (nullable, f32
+ * [n_chunks]) receives each chunk's sum of squared raw gradients.
+ * ---------------------------------------------------------------------- */
+int gptrig_adamw(float* param, const float* grad, float* m, float* v, void* param_bf16, const int32_t* chunk_tensor,
+                 const float* tensor_hparams, int64_t n_chunks, int chunk, float lr, float beta1, float beta2,
+                 int step, const float* clip_scale, float* sq_partials, void* stream);
+/* Per-chunk sums of squares of an f32 arena (for clipping before the update). */
+int gptrig_sq_norm_partials(const float* x, int64_t n_chunks, int chunk, float* partials, void* stream);
+/* norm = sqrt(sum partials); clip = min(1, grad_clip/(norm+1e-6)) (1 if grad_clip <= 0);
+ * history_row (nullable) = {*loss, lr, norm} (train.py:1446-1447). */
+int gptrig_finalize_norm(const float* partials, int parts, float grad_clip, float* norm_out, float* clip_out,
+                         const float* loss, float lr, float* history_row, void* stream);
+
+/* Small helpers of the step: f32 -> bf16 cast, out += weight * sum(x), fill. */
+int gptrig_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream);
+int gptrig_weighted_sum(const float* x, int64_t n, float weight, float* out, void* stream);
+int gptrig_fill_f32(float* x, int64_t n, float value, void* stream);
+
+/* ------------------------------------------------------------------------
+ * MoE routing: recipes/reference_moe/train.py:1259-1273 (routed_mlp_local).
+ * logits f32 [tokens, experts] (experts <= 64, top_k <= experts):
+ *   probs f32 [tokens, experts] = softmax(logits)          (nullable)
+ *   chosen i32 [tokens, top_k] = jax.lax.top_k indices (descending value,
+ *     lower index first on ties), gate f32 [tokens, top_k] = softmax of the
+ *     chosen logits;
+ *   counts i32 [experts] = assignments per expert;
+ *   order i32 [tokens*top_k] = stable argsort of chosen.reshape(-1);
+ *   rows i32 [tokens*top_k] = order / top_k (the source token of each slot).
+ * workspace: gptrig_moe_route_workspace_bytes(tokens, experts, top_k).
+ * ---------------------------------------------------------------------- */
+size_t gptrig_moe_route_workspace_bytes(int tokens, int experts, int top_k);
+int gptrig_moe_route(const float* logits, float* probs, int32_t* chosen, float* gate, int32_t* counts,
+                     int32_t* order, int32_t* rows, void* workspace, size_t workspace_bytes, int tokens, int experts,
+                     int top_k, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPTRIG_H_ */
