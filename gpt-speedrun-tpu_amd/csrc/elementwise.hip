@@ -10,12 +10,21 @@ namespace {
 
 constexpr int kWave = 64;
 
+__global__ void fill_f32_kernel(float* __restrict__ x, int64_t n, float value) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = value;
+}
+
 // ----------------------------------------------------------------------------
 // RMSNorm  (rig/nn.py:26-33)
 //   n  = bf16(x * rsqrt(mean(x^2) + 1e-5))      statistic in fp32
 //   y  = bf16(n * scale_bf16)
-// One wave per row; rstd saved for the backward.
+// One wave per row, 4-element (8-byte) vectors; a lane always owns the same
+// columns (c = lane + 64t), so the backward keeps its dscale partial in
+// registers across rows.  kMaxChunks bounds the per-lane row cache (d <= 2048).
 // ----------------------------------------------------------------------------
+constexpr int kMaxChunks = 8;
+
 __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ scale,
                                                           bf16* __restrict__ y, float* __restrict__ rstd, int rows,
                                                           int d) {
@@ -24,41 +33,30 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* __restrict
   if (row >= rows) return;
   const bf16* xr = x + (size_t)row * d;
   bf16* yr = y + (size_t)row * d;
+  const int chunks = d / 4;
+  bf16x4 xv[kMaxChunks];
   float ss = 0.f;
-  if ((d & 7) == 0) {
-    for (int c = lane; c < d / 8; c += kWave) {
-      bf16x8 v = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float f = (float)v[j];
-        ss += f * f;
-      }
-    }
-  } else {
-    for (int c = lane; c < d; c += kWave) {
-      float f = (float)xr[c];
-      ss += f * f;
+  for (int t = 0; t < kMaxChunks; ++t) {
+    const int c = lane + kWave * t;
+    if (c < chunks) {
+      xv[t] = *reinterpret_cast<const bf16x4*>(xr + 4 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss += (float)xv[t][j] * (float)xv[t][j];
     }
   }
   ss = wave_sum(ss);
   const float r = rsqrtf(ss / (float)d + 1.0e-5f);
   if (lane == 0 && rstd) rstd[row] = r;
-  if ((d & 7) == 0) {
-    for (int c = lane; c < d / 8; c += kWave) {
-      bf16x8 v = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
-      bf16x8 s = *reinterpret_cast<const bf16x8*>(scale + 8 * c);
-      bf16x8 o;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float n = (float)(bf16)((float)v[j] * r);
-        o[j] = (bf16)(n * (float)s[j]);
-      }
-      *reinterpret_cast<bf16x8*>(yr + 8 * c) = o;
-    }
-  } else {
-    for (int c = lane; c < d; c += kWave) {
-      float n = (float)(bf16)((float)xr[c] * r);
-      yr[c] = (bf16)(n * (float)scale[c]);
+  for (int t = 0; t < kMaxChunks; ++t) {
+    const int c = lane + kWave * t;
+    if (c < chunks) {
+      bf16x4 sv = *reinterpret_cast<const bf16x4*>(scale + 4 * c);
+      bf16x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (bf16)((float)(bf16)((float)xv[t][j] * r) * (float)sv[j]);
+      *reinterpret_cast<bf16x4*>(yr + 4 * c) = o;
     }
   }
 }
@@ -67,7 +65,7 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* __restrict
 //   dn = bf16(dy * scale)                       (cotangent of the bf16 product)
 //   dx = r*dn - (r^3/d) * x * sum_j(dn_j x_j)   (fp32), rounded to bf16
 //   dx += dresidual (bf16 add), if given
-//   dscale_partial[block][j] = sum over the block's rows of dy_j * n_j
+//   partial[block][j] = sum over the block's rows of dy_j * n_j
 __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x,
                                                           const bf16* __restrict__ scale,
                                                           const float* __restrict__ rstd,
@@ -77,29 +75,58 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const bf16* __restrict
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x / kWave;
   const int waves = blockDim.x / kWave;
-  float* my = smem + (size_t)wave * d;
-  for (int j = lane; j < d; j += kWave) my[j] = 0.f;
+  const int chunks = d / 4;
+  f32x4 dsc[kMaxChunks];
+  bf16x4 sv[kMaxChunks];
+#pragma unroll
+  for (int t = 0; t < kMaxChunks; ++t) {
+    dsc[t] = f32x4{};
+    const int c = lane + kWave * t;
+    if (c < chunks) sv[t] = *reinterpret_cast<const bf16x4*>(scale + 4 * c);
+  }
   for (int row = blockIdx.x * waves + wave; row < rows; row += gridDim.x * waves) {
     const bf16* xr = x + (size_t)row * d;
     const bf16* gr = dy + (size_t)row * d;
     const float r = rstd[row];
+    bf16x4 xv[kMaxChunks], gv[kMaxChunks];
     float dot = 0.f;
-    for (int j = lane; j < d; j += kWave) {
-      float dn = (float)(bf16)((float)gr[j] * (float)scale[j]);
-      dot += dn * (float)xr[j];
+#pragma unroll
+    for (int t = 0; t < kMaxChunks; ++t) {
+      const int c = lane + kWave * t;
+      if (c < chunks) {
+        xv[t] = *reinterpret_cast<const bf16x4*>(xr + 4 * c);
+        gv[t] = *reinterpret_cast<const bf16x4*>(gr + 4 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot += (float)(bf16)((float)gv[t][j] * (float)sv[t][j]) * (float)xv[t][j];
+      }
     }
     dot = wave_sum(dot);
     const float coef = r * r * r * dot / (float)d;
     bf16* o = dx + (size_t)row * d;
-    for (int j = lane; j < d; j += kWave) {
-      float xv = (float)xr[j];
-      float g = (float)gr[j];
-      float dn = (float)(bf16)(g * (float)scale[j]);
-      float v = (float)(bf16)(r * dn - coef * xv);
-      if (dres) v += (float)dres[(size_t)row * d + j];
-      o[j] = (bf16)v;
-      my[j] += g * (float)(bf16)(xv * r);
+#pragma unroll
+    for (int t = 0; t < kMaxChunks; ++t) {
+      const int c = lane + kWave * t;
+      if (c < chunks) {
+        bf16x4 rv;
+        if (dres) rv = *reinterpret_cast<const bf16x4*>(dres + (size_t)row * d + 4 * c);
+        bf16x4 ov;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float xf = (float)xv[t][j], g = (float)gv[t][j];
+          const float dn = (float)(bf16)(g * (float)sv[t][j]);
+          float v = (float)(bf16)(r * dn - coef * xf);
+          if (dres) v += (float)rv[j];
+          ov[j] = (bf16)v;
+          dsc[t][j] += g * (float)(bf16)(xf * r);
+        }
+        *reinterpret_cast<bf16x4*>(o + 4 * c) = ov;
+      }
     }
+  }
+#pragma unroll
+  for (int t = 0; t < kMaxChunks; ++t) {
+    const int c = lane + kWave * t;
+    if (c < chunks) *reinterpret_cast<f32x4*>(smem + (size_t)wave * d + 4 * c) = dsc[t];
   }
   __syncthreads();
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
@@ -109,13 +136,58 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const bf16* __restrict
   }
 }
 
-__global__ void column_sum_kernel(const float* __restrict__ partial, int parts, int d, float* __restrict__ out,
-                                  int accumulate) {
-  int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= d) return;
+// out[j] (+)= sum_p partial[p][j]: 64 columns x 4 part-slices per block, the
+// part range split over gridDim.y, one atomic per column per block.
+__global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict__ partial, int parts, int d,
+                                                         float* __restrict__ out) {
+  __shared__ float red[4][64];
+  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int slice = threadIdx.x >> 6;
+  const int per = (parts + gridDim.y - 1) / gridDim.y;
+  const int p0 = blockIdx.y * per, p1 = min(parts, p0 + per);
   float s = 0.f;
-  for (int p = 0; p < parts; ++p) s += partial[(size_t)p * d + j];
-  out[j] = accumulate ? out[j] + s : s;
+  if (col < d)
+    for (int p = p0 + slice; p < p1; p += 4) s += partial[(size_t)p * d + col];
+  red[slice][threadIdx.x & 63] = s;
+  __syncthreads();
+  if (slice == 0 && col < d) atomicAdd(out + col, red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] +
+                                                      red[3][threadIdx.x]);
+}
+
+// Bias gradient: db[j] += sum_rows dy[row][j] in fp32 (the transpose of the
+// broadcast bias add of rig/nn.py:55-56).  8 columns per thread, 64 column
+// chunks x 4 row slices per block, rows split over gridDim.y.
+__global__ void __launch_bounds__(256) bias_grad_kernel(const bf16* __restrict__ dy, int rows, int cols,
+                                                        float* __restrict__ db) {
+  __shared__ f32x4 red[4][64][2];
+  const int cc = blockIdx.x * 64 + (threadIdx.x & 63);  // 8-column chunk
+  const int slice = threadIdx.x >> 6;
+  const int per = (rows + gridDim.y - 1) / gridDim.y;
+  const int r0 = blockIdx.y * per, r1 = min(rows, r0 + per);
+  f32x4 a = f32x4{}, b = f32x4{};
+  if (8 * cc < cols) {
+    for (int r = r0 + slice; r < r1; r += 4) {
+      bf16x8 v = *reinterpret_cast<const bf16x8*>(dy + (size_t)r * cols + 8 * cc);
+      a[0] += (float)v[0]; a[1] += (float)v[1]; a[2] += (float)v[2]; a[3] += (float)v[3];
+      b[0] += (float)v[4]; b[1] += (float)v[5]; b[2] += (float)v[6]; b[3] += (float)v[7];
+    }
+  }
+  red[slice][threadIdx.x & 63][0] = a;
+  red[slice][threadIdx.x & 63][1] = b;
+  __syncthreads();
+  if (slice == 0 && 8 * cc < cols) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      f32x4 t = red[0][threadIdx.x][h];
+#pragma unroll
+      for (int s2 = 1; s2 < 4; ++s2) {
+        f32x4 u = red[s2][threadIdx.x][h];
+        t[0] += u[0]; t[1] += u[1]; t[2] += u[2]; t[3] += u[3];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) atomicAdd(db + 8 * cc + 4 * h + j, t[j]);
+    }
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -375,10 +447,6 @@ __global__ void __launch_bounds__(256) weighted_sum_kernel(const float* __restri
   if (threadIdx.x == 0) atomicAdd(out, weight * (red[0] + red[1] + red[2] + red[3]));
 }
 
-__global__ void fill_f32_kernel(float* __restrict__ x, int64_t n, float value) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) x[i] = value;
-}
 
 }  // namespace
 
@@ -389,35 +457,53 @@ extern "C" {
 
 int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, int rows, int d, void* stream) {
   if (!x || !scale || !y) return GPTRIG_E_NULL;
-  if (rows < 0 || d <= 0) return GPTRIG_E_SHAPE;
+  if (rows < 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
+  if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
   if (rows == 0) return GPTRIG_OK;
-  dim3 block(256);
-  dim3 grid(ceil_div(rows, 4));
-  rmsnorm_fwd_kernel<<<grid, block, 0, (hipStream_t)stream>>>((const bf16*)x, (const bf16*)scale, (bf16*)y, rstd,
-                                                               rows, d);
+  rmsnorm_fwd_kernel<<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>((const bf16*)x, (const bf16*)scale,
+                                                                          (bf16*)y, rstd, rows, d);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
 
+static int rmsnorm_bwd_blocks(int rows) {
+  const int b = ceil_div(rows, 16);
+  return b < 1 ? 1 : (b > 1024 ? 1024 : b);
+}
+
 size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d) {
-  int blocks = rows < 4 ? 1 : (ceil_div(rows, 4) < 1024 ? ceil_div(rows, 4) : 1024);
-  return (size_t)blocks * d * sizeof(float);
+  return (size_t)rmsnorm_bwd_blocks(rows) * d * sizeof(float);
 }
 
 int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const float* rstd, const void* dresidual,
                        void* dx, float* dscale, int accumulate_dscale, void* workspace, size_t workspace_bytes,
                        int rows, int d, void* stream) {
   if (!dy || !x || !scale || !rstd || !dx || !dscale || !workspace) return GPTRIG_E_NULL;
-  if (rows <= 0 || d <= 0) return GPTRIG_E_SHAPE;
-  if ((size_t)d * 4 * sizeof(float) > 64 * 1024) return GPTRIG_E_UNSUPPORTED;
+  if (rows <= 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
+  if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
   if (workspace_bytes < gptrig_rmsnorm_bwd_workspace_bytes(rows, d)) return GPTRIG_E_WORKSPACE;
-  int blocks = rows < 4 ? 1 : (ceil_div(rows, 4) < 1024 ? ceil_div(rows, 4) : 1024);
+  const int blocks = rmsnorm_bwd_blocks(rows);
   hipStream_t s = (hipStream_t)stream;
+  if (!accumulate_dscale) {
+    fill_f32_kernel<<<ceil_div(d, 256), 256, 0, s>>>(dscale, d, 0.f);
+    GPTRIG_CHECK_LAUNCH();
+  }
   rmsnorm_bwd_kernel<<<blocks, 256, 4 * d * sizeof(float), s>>>((const bf16*)dy, (const bf16*)x, (const bf16*)scale,
                                                                   rstd, (const bf16*)dresidual, (bf16*)dx,
                                                                   (float*)workspace, rows, d);
   GPTRIG_CHECK_LAUNCH();
-  column_sum_kernel<<<ceil_div(d, 256), 256, 0, s>>>((const float*)workspace, blocks, d, dscale, accumulate_dscale);
+  column_sum_kernel<<<dim3(ceil_div(d, 64), 16), 256, 0, s>>>((const float*)workspace, blocks, d, dscale);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_bias_grad(const void* dy, int rows, int cols, float* db, void* stream) {
+  if (!dy || !db) return GPTRIG_E_NULL;
+  if (rows < 0 || cols <= 0 || cols % 8) return GPTRIG_E_SHAPE;
+  if (rows == 0) return GPTRIG_OK;
+  const int ysplit = (rows + 127) / 128;
+  bias_grad_kernel<<<dim3(ceil_div(cols / 8, 64), ysplit), 256, 0, (hipStream_t)stream>>>((const bf16*)dy, rows,
+                                                                                          cols, db);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

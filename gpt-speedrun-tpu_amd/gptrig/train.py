@@ -16,8 +16,9 @@ Memory layout (HBM):
 
 The forward and backward passes are explicit (no autograd tape): RMSNorm,
 RoPE, attention, GELU, the LM-head cross-entropy, the embedding scatter and
-AdamW are HIP kernels; the dense projections are hipBLASLt GEMMs through
-torch.  Weight gradients accumulate in float32 across micro-batches; the
+AdamW are HIP kernels; the forward and input-gradient projections are
+hipBLASLt GEMMs through torch, the weight gradients the HIP GEMM with
+split-K float32 accumulation into the gradient arena.  Weight gradients accumulate in float32 across micro-batches; the
 global batch is split into equal micro-batches whose mean losses are averaged,
 which equals the reference's single-batch token mean.
 """
@@ -280,7 +281,7 @@ class GPTTrainer:
         _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
 
         # ---- backward ----
-        chunk = lce.chunk_for(c.vocab_tile_size if c.vocab_tile_size > 2048 else 4096)
+        chunk = lce.chunk_for(c.vocab_tile_size if c.vocab_tile_size > 2048 else 8192)
         ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
         dxf = torch.empty((N, d), dtype=BF16, device=self.device)
         with self._timed("flce"):
@@ -322,11 +323,11 @@ class GPTTrainer:
         """dW += inp^T dout and db += sum_rows(dout), both float32."""
 
         A = self.arena
-        gw = A.grad(prefix + "_w")
-        # hipBLASLt: bf16 operands, float32 accumulator read and written in place.
-        torch.addmm(gw, inp.t(), dout, out_dtype=F32, out=gw)
-        gb = A.grad(prefix + "_b")
-        gb.add_(dout.sum(0, dtype=F32))
+        n, rows_in = inp.shape
+        _lib.call("gptrig_weight_grad", inp.data_ptr(), dout.data_ptr(), A.grad(prefix + "_w").data_ptr(), n, rows_in,
+                  dout.shape[1], _lib.stream())
+        _lib.call("gptrig_bias_grad", dout.data_ptr(), dout.shape[0], dout.shape[1], A.grad(prefix + "_b").data_ptr(),
+                  _lib.stream())
 
     # -- the step ----------------------------------------------------------------------
     def train_step(self, x: torch.Tensor, y: torch.Tensor) -> None:

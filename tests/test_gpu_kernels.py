@@ -340,3 +340,29 @@ def test_moe_routing_bit_exact():
     assert torch.equal(rows.cpu().long(), rows_r)
     assert float((gate.cpu() - gate_r).abs().max()) <= 1e-6
     assert float((probs.cpu() - probs_r).abs().max()) <= 1e-6
+
+
+def test_bias_grad_column_sum():
+    from gptrig import _lib
+
+    for rows, cols in ((5000, 2304), (7, 64), (4096, 768)):
+        dy = randn((rows, cols), 101)
+        db = torch.full((cols,), 0.5, device=DEV)
+        dyg = dy.to(DEV)
+        _lib.call("gptrig_bias_grad", dyg.data_ptr(), rows, cols, db.data_ptr(), _lib.stream())
+        want = dy.double().sum(0) + 0.5
+        assert float((db.cpu().double() - want).abs().max()) <= 1e-3
+
+
+def test_weight_grad_split_k_gemm():
+    from gptrig import _lib
+
+    for n, rin, cout in ((4096, 768, 2304), (1000, 64, 200), (8192, 3072, 768)):
+        x = randn((n, rin), 111)
+        dy = randn((n, cout), 112)
+        dw = torch.full((rin, cout), 0.25, device=DEV)
+        xg, dyg = x.to(DEV), dy.to(DEV)  # keep the device copies alive across the call
+        _lib.call("gptrig_weight_grad", xg.data_ptr(), dyg.data_ptr(), dw.data_ptr(), n, rin, cout, _lib.stream())
+        want = x.double().t() @ dy.double() + 0.25
+        err = float((dw.cpu().double() - want).abs().max())
+        assert err <= 1e-3 * float(want.abs().max()), (n, rin, cout, err)
