@@ -19,7 +19,7 @@
 // dK^T += Q^T dS in registers, and publishes bf16 dS to LDS; the workgroup
 // then forms dQ = dS K (all 128 keys) and adds it to an fp32 accumulator with
 // atomics.  A last pass rounds dQ to bf16.
-#include "common.h"
+#include "attn64.h"
 
 namespace {
 
@@ -498,6 +498,389 @@ __global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView
   *reinterpret_cast<bf16x8*>(dQ.row(bh / H, bh % H, s) + 8 * c) = o;
 }
 
+
+// ============================================================================
+// head_dim 64 kernels on swizzled row-major LDS tiles (attn64.h)
+// ============================================================================
+__device__ const bf16x8 kZeroChunk[2] = {};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
+
+// Forward: K/V tiles of 64 keys are copied global -> LDS by the DMA path
+// (global_load_lds_dwordx4) into double-buffered swizzled tiles; V^T operands
+// come from transposed reads with the accumulator's row order.
+template <bool kSeg>
+__global__ void __launch_bounds__(256, 2)
+    attn_fwd64_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
+                      int B, int H, int S, float scale_log2) {
+  constexpr int D = 64, KC = 4, DB = 2, TILE = 64 * 64;
+  __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K[2], V[2]
+  at64::lds_t* const Kt = gemm::lds_cast(smem);
+  at64::lds_t* const Vt = Kt + 2 * TILE;
+
+  const int nq = (S + kBlockM - 1) / kBlockM;
+  int bh, qb;
+  xcd_map(blockIdx.x, nq, B * H, bh, qb);
+  qb = nq - 1 - qb;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int q0 = qb * kBlockM;
+  const int qw0 = q0 + wave * 32;
+  const int my_q = qw0 + l32;
+  const int last_q = min(q0 + kBlockM, S) - 1;
+  const int ntiles = last_q / kBlockN + 1;
+
+  bf16x8 qreg[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+    qreg[kc] = my_q < S ? *reinterpret_cast<const bf16x8*>(Q.row(b, h, my_q) + 16 * kc + 8 * hl) : bf16x8{};
+  const int seg_q = (kSeg && my_q < S) ? seg[(size_t)b * S + my_q] : 0;
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  float m_run = kMinusBig, l_run = 0.f;
+
+  // Wave w fills 1 KB blocks 2w, 2w+1 (8 rows each) of the K and V tiles.
+  auto fill = [&](int buf, int kv0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int blk = 2 * wave + j;
+      const int row = 8 * blk + (lane >> 3);
+      const int t = (row >> 1) & 7;
+      const int c = (lane & 7) ^ (((t & 1) << 2) | (t >> 1));
+      const bool ok = kv0 + row < S;
+      const bf16* ks = ok ? K.row(b, h, kv0 + row) + 8 * c : (const bf16*)kZeroChunk;
+      const bf16* vs = ok ? V.row(b, h, kv0 + row) + 8 * c : (const bf16*)kZeroChunk;
+      __builtin_amdgcn_global_load_lds((gbl_void*)ks, (lds_void*)(Kt + buf * TILE + blk * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void*)vs, (lds_void*)(Vt + buf * TILE + blk * 512), 16, 0, 0);
+    }
+  };
+
+  fill(0, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int kv0 = it * kBlockN;
+    const at64::lds_t* kt = Kt + buf * TILE;
+    const at64::lds_t* vt = Vt + buf * TILE;
+    const bool active = kv0 <= qw0 + 31;  // some key of this tile is visible to this wave
+    // All reads of this tile are issued before the prefetch into the other
+    // buffer, so no LDS-DMA ordering wait separates them.
+    bf16x8 kf[2][KC], vf[DB][4];
+    if (active) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) kf[sb][kc] = at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) vf[db][c] = at64::trfrag<true>(vt, 32 * db, 16 * c, lane);
+    }
+    if (it + 1 < ntiles) fill(buf ^ 1, kv0 + kBlockN);
+
+    if (active) {
+      f32x16 s[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        s[sb] = f32x16{};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) s[sb] = mfma32(kf[sb][kc], qreg[kc], s[sb]);
+      }
+      // Row max on raw scores (scale > 0); masked scores become -inf.
+      const bool need_mask = (kv0 + kBlockN - 1 > qw0) || (kv0 + kBlockN > S) || kSeg;
+      float mraw = -INFINITY;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (need_mask) {
+            const int key = kv0 + 32 * sb + 8 * (i >> 2) + 4 * hl + (i & 3);
+            bool vis = key <= my_q && key < S;
+            if (kSeg && vis) vis = seg[(size_t)b * S + key] == seg_q;
+            s[sb][i] = vis ? s[sb][i] : -INFINITY;
+          }
+          mraw = fmaxf(mraw, s[sb][i]);
+        }
+      }
+      mraw = fmaxf(mraw, __shfl_xor(mraw, 32));
+      // Lazy rescaling: the running max (log2 units) only moves when a row's
+      // max exceeds it by more than 8, so probabilities stay <= 2^8 and the
+      // accumulator rescale is skipped on most tiles.  O = acc / l and
+      // lse = m + log2(l) hold for any consistent m.
+      const float m_tile = mraw * scale_log2;
+      const bool grow = m_tile > m_run + 8.0f;
+      const float m_new = grow ? m_tile : m_run;
+      if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+      }
+      m_run = m_new;
+      float lsum = 0.f;
+      bf16x8 pb[4];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float p = fast_exp2(fmaf(s[sb][8 * c2 + j], scale_log2, -m_new));
+            lsum += p;
+            pb[2 * sb + c2][j] = (bf16)p;
+          }
+      l_run += lsum;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db] = mfma32(vf[db][c], pb[c], acc[db]);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (my_q < S) {
+    const float inv = 1.0f / l_tot;
+    bf16* orow = O.row(b, h, my_q);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16x4 o4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o4[t] = (bf16)(acc[db][4 * r + t] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * db + 8 * r + 4 * hl) = o4;
+      }
+    if (hl == 0) lse[((size_t)b * H + h) * S + my_q] = (m_run + __log2f(l_tot)) * GPTRIG_LN2;
+  }
+}
+
+// Backward: KV-owned, 128 keys per workgroup (32 per wave), 64 queries per
+// step.  Q/dO/K tiles are swizzled row-major; Q^T, dO^T, K^T and dS come from
+// transposed reads, so nothing is written to LDS transposed.  dS is stored as
+// dS^T [key][query] (8-byte writes) and dQ = dS K is added to an fp32
+// accumulator with atomics.
+template <bool kSeg>
+__global__ void __launch_bounds__(256, 2)
+    attn_bwd64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
+                      const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
+                      MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2) {
+  constexpr int D = 64, KC = 4, DB = 2;
+  __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 128 + 128) * 64];
+  __shared__ __attribute__((aligned(16))) float lse_s[kBwdM], delta_s[kBwdM];
+  __shared__ int seg_s[kBwdM];
+  at64::lds_t* const Qs = gemm::lds_cast(smem);
+  at64::lds_t* const dOs = Qs + 64 * 64;
+  at64::lds_t* const Ks = dOs + 64 * 64;
+  at64::lds_t* const dSt = Ks + 128 * 64;
+
+  const int nkv = (S + kBwdN - 1) / kBwdN;
+  int bh, kb;
+  xcd_map(blockIdx.x, nkv, B * H, bh, kb);
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int k0 = kb * kBwdN;
+  const int kw0 = k0 + 32 * wave;
+  const int my_k = kw0 + l32;
+  const bool k_ok = my_k < S;
+
+  bf16x8 kreg[KC], vreg[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    kreg[kc] = k_ok ? *reinterpret_cast<const bf16x8*>(K.row(b, h, my_k) + 16 * kc + 8 * hl) : bf16x8{};
+    vreg[kc] = k_ok ? *reinterpret_cast<const bf16x8*>(V.row(b, h, my_k) + 16 * kc + 8 * hl) : bf16x8{};
+  }
+  const int seg_k = (kSeg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
+
+  // K tile of the workgroup's 128 keys (row-major, swizzled) for dQ = dS K.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int idx = tid + 256 * r;
+    const int row = idx >> 3, c = idx & 7;
+    const bf16x8 kv = k0 + row < S ? *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + row) + 8 * c) : bf16x8{};
+    *(at64::lds_x8*)(Ks + at64::swz(row, c)) = kv;
+  }
+
+  f32x16 dv_acc[DB], dk_acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dv_acc[db] = f32x16{};
+    dk_acc[db] = f32x16{};
+  }
+  const float* lse_bh = lse + (size_t)bh * S;
+  const float* delta_bh = delta + (size_t)bh * S;
+  float* dq_bh = dq_acc + (size_t)bh * S * D;
+
+  // Register staging of one 64-query block: 2 x 16 B of Q and of dO per thread.
+  bf16x8 qst[2], gst[2];
+  float lse_st = 0.f, delta_st = 0.f;
+  int seg_st = 0;
+  auto load_q = [&](int qq0) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int idx = tid + 256 * r;
+      const int qi = idx >> 3, c = idx & 7;
+      const bool ok = qq0 + qi < S;
+      qst[r] = ok ? *reinterpret_cast<const bf16x8*>(Q.row(b, h, qq0 + qi) + 8 * c) : bf16x8{};
+      gst[r] = ok ? *reinterpret_cast<const bf16x8*>(dO.row(b, h, qq0 + qi) + 8 * c) : bf16x8{};
+    }
+    if (tid < kBwdM) {
+      const int q = qq0 + tid;
+      lse_st = q < S ? lse_bh[q] * GPTRIG_LOG2E : 0.f;
+      delta_st = q < S ? delta_bh[q] * scale : 0.f;  // pre-scaled: dS = P * (scale*dP - scale*Delta)
+      if (kSeg) seg_st = q < S ? seg[(size_t)b * S + q] : 0;
+    }
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int idx = tid + 256 * r;
+      const int qi = idx >> 3, c = idx & 7;
+      *(at64::lds_x8*)(Qs + at64::swz(qi, c)) = qst[r];
+      *(at64::lds_x8*)(dOs + at64::swz(qi, c)) = gst[r];
+    }
+    if (tid < kBwdM) {
+      lse_s[tid] = lse_st;
+      delta_s[tid] = delta_st;
+      if (kSeg) seg_s[tid] = seg_st;
+    }
+  };
+
+  const int qb_first = k0 / kBwdM;
+  const int nqb = (S + kBwdM - 1) / kBwdM;
+  load_q(qb_first * kBwdM);
+
+  for (int qb = qb_first; qb < nqb; ++qb) {
+    const int qq0 = qb * kBwdM;
+    store_q();
+    __syncthreads();  // (A) Q, dO, lse, delta of this block published
+    // Unconditional prefetch (the last step re-reads its own block) keeps the
+    // memory-counter state identical on every iteration, so the wait for it is
+    // exact instead of draining the dQ atomics too.
+    load_q(qb + 1 < nqb ? qq0 + kBwdM : qq0);
+
+    const bool wave_active = kw0 <= qq0 + kBwdM - 1 && kw0 < S;
+    if (!wave_active) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, c) + 4 * hl) = bf16x4{};
+    } else {
+      const bool need_mask = (qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || kSeg;
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        bf16x8 qf[KC], gf[KC];
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          qf[kc] = at64::rowfrag(Qs, 32 * qs + l32, 2 * kc + hl);
+          gf[kc] = at64::rowfrag(dOs, 32 * qs + l32, 2 * kc + hl);
+        }
+        f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          sacc = mfma32(qf[kc], kreg[kc], sacc);
+          pacc = mfma32(gf[kc], vreg[kc], pacc);
+        }
+        // Transposed operands of dV^T += dO^T P and dK^T += Q^T dS, read while
+        // the softmax below runs on the VALU.
+        bf16x8 gt[DB][2], qt[DB][2];
+#pragma unroll
+        for (int dbk = 0; dbk < DB; ++dbk)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            gt[dbk][c] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
+            qt[dbk][c] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
+          }
+        bf16x8 pb[2], db8[2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qr = 32 * qs + 8 * r + 4 * hl;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse_s[qr]);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&delta_s[qr]);
+          bf16x4 ds4;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int i = 4 * r + t;
+            float p = fast_exp2(fmaf(sacc[i], scale_log2, -l4[t]));
+            if (need_mask) {
+              const int q = qq0 + qr + t;
+              bool vis = my_k <= q && q < S && k_ok;
+              if (kSeg && vis) vis = seg_s[qr + t] == seg_k;
+              p = vis ? p : 0.f;
+            }
+            const float ds = p * fmaf(pacc[i], scale, -d4[t]);
+            pb[i >> 3][i & 7] = (bf16)p;
+            const bf16 dsb = (bf16)ds;
+            db8[i >> 3][i & 7] = dsb;
+            ds4[t] = dsb;
+          }
+          // dS^T row = this lane's key, queries 32qs + 8r + 4hl .. +3.
+          *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, 4 * qs + r) + 4 * hl) = ds4;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int dbk = 0; dbk < DB; ++dbk) {
+            dv_acc[dbk] = mfma32(gt[dbk][c], pb[c], dv_acc[dbk]);
+            dk_acc[dbk] = mfma32(qt[dbk][c], db8[c], dk_acc[dbk]);
+          }
+      }
+    }
+    __syncthreads();  // (B) dS^T published
+
+    {  // dQ tile of this wave: queries 32*(wave/2).., d 32*(wave%2).. over the 128 keys.
+      const int qs = wave >> 1, dblk = wave & 1;
+      f32x16 dq = f32x16{};
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        bf16x8 af[4], bfk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          af[j] = at64::trfrag<false>(dSt, 32 * qs, 16 * (4 * half + j), lane);
+          bfk[j] = at64::trfrag<false>(Ks, 32 * dblk, 16 * (4 * half + j), lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dq = mfma32(af[j], bfk[j], dq);
+      }
+      const int dcol = 32 * dblk + l32;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int q = qq0 + 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (q < S) atomicAdd(dq_bh + (size_t)q * D + dcol, dq[i]);
+      }
+    }
+    // The next block's store_q only touches Q/dO (last read before (B)); its
+    // dS^T writes come after the next (A), which every wave reaches only after
+    // finishing this dQ step.
+  }
+
+  if (k_ok) {
+    bf16* dvrow = dV.row(b, h, my_k);
+    bf16* dkrow = dK.row(b, h, my_k);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16x4 v4, k4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          v4[t] = (bf16)dv_acc[db][4 * r + t];
+          k4[t] = (bf16)dk_acc[db][4 * r + t];
+        }
+        *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * r + 4 * hl) = v4;
+        *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * r + 4 * hl) = k4;
+      }
+  }
+}
+
 bool strides_ok(const int64_t* st, int n) {
   // Row starts must stay 16-byte aligned for the vector loads.
   for (int i = 0; i < 3 * n; ++i)
@@ -539,7 +922,12 @@ int gptrig_attn_fwd(const void* q, const void* k, const void* v, const int32_t* 
   const float sl2 = softmax_scale * GPTRIG_LOG2E;
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 64)
-    attn_fwd_kernel<64><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
+  {
+    if (segment_ids)
+      attn_fwd64_kernel<true><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
+    else
+      attn_fwd64_kernel<false><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, nullptr, batch, heads, seq, sl2);
+  }
   else
     attn_fwd_kernel<128><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
   GPTRIG_CHECK_LAUNCH();
@@ -585,8 +973,12 @@ int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
     attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
                                                                                 seq);
     GPTRIG_CHECK_LAUNCH();
-    attn_bwd_kernel<64><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV, batch,
-                                                       heads, seq, softmax_scale, sl2);
+    if (segment_ids)
+      attn_bwd64_kernel<true><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV,
+                                                             batch, heads, seq, softmax_scale, sl2);
+    else
+      attn_bwd64_kernel<false><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, nullptr, dq_acc, dK, dV, batch,
+                                                              heads, seq, softmax_scale, sl2);
     GPTRIG_CHECK_LAUNCH();
     attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq);
   } else {

@@ -20,7 +20,7 @@ namespace gemm {
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int THREADS = 512;
 constexpr int KLD = BK + 8;         // K-major LDS row stride (elements), 144 B rows
-constexpr int MLD = 256 + 16;       // MN-major LDS row stride, 544 B rows (== 8 dwords mod 64 banks)
+constexpr int MLD = 256 + 32;       // MN-major LDS row stride: 576 B rows, 144 dwords == 16 (mod 64 banks)
 constexpr int SLAB = 256 * KLD;     // elements per operand per stage (>= BK * MLD)
 static_assert(BK * MLD <= SLAB, "MN-major slab must fit");
 constexpr int LDS_BYTES = 4 * SLAB * 2;
@@ -95,9 +95,18 @@ __device__ __forceinline__ bf16x8 frag(const lds_t* lds, int r0, int kc, int lan
   }
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
+// Give XCD x a contiguous range of logical tile ids so that the tiles sharing
+// A/B slabs run on the same L2.
+__device__ __forceinline__ int xcd_swizzle(int pid, int total) {
+  const int q = total >> 3, r = total & 7, x = pid & 7;
+  return x * q + min(x, r) + (pid >> 3);
+}
+
 // Grouped tile order: kGroupM M-tiles share each N sweep so their B slabs stay in L2.
 __device__ __forceinline__ void tile_coords(int pid, int M, int N, int& tm, int& tn) {
   const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+  pid = xcd_swizzle(pid, mt * nt);
   const int in_group = kGroupM * nt;
   const int group = pid / in_group;
   const int first_m = group * kGroupM;
