@@ -1,4 +1,4 @@
-"""Benchmark: one-GPU training step of the reference 125M GPT (BASELINE config D).
+"""Benchmark: one-GPU training step of the reference 125M GPT (12 layers, d_model 768).
 
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
 

@@ -166,6 +166,7 @@ __global__ void __launch_bounds__(256) bias_grad_kernel(const bf16* __restrict__
   const int r0 = blockIdx.y * per, r1 = min(rows, r0 + per);
   f32x4 a = f32x4{}, b = f32x4{};
   if (8 * cc < cols) {
+#pragma unroll 8
     for (int r = r0 + slice; r < r1; r += 4) {
       bf16x8 v = *reinterpret_cast<const bf16x8*>(dy + (size_t)r * cols + 8 * cc);
       a[0] += (float)v[0]; a[1] += (float)v[1]; a[2] += (float)v[2]; a[3] += (float)v[3];
@@ -467,8 +468,9 @@ int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, i
 }
 
 static int rmsnorm_bwd_blocks(int rows) {
-  const int b = ceil_div(rows, 16);
-  return b < 1 ? 1 : (b > 1024 ? 1024 : b);
+  // About two rows per wave: enough waves in flight to cover HBM latency.
+  const int b = ceil_div(rows, 8);
+  return b < 1 ? 1 : (b > 4096 ? 4096 : b);
 }
 
 size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d) {

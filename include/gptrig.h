@@ -13,8 +13,7 @@
  *   - "bf16" buffers hold bfloat16, "f32" float32, "i32" int32.
  *
  * Each entry point maps 1:1 onto an XLA-FFI custom-call handler (buffers,
- * stream, scalar attributes); see INTEGRATION.md for the reference-side
- * binding.
+ * stream, scalar attributes) or a ctypes call from a torch front end.
  */
 #ifndef GPTRIG_H_
 #define GPTRIG_H_

@@ -92,7 +92,7 @@ def smoke_config() -> Config:
 
 
 def baseline_config(name: str, steps: int = 20) -> Config:
-    """The five BASELINE configurations' model/optimizer fields."""
+    """Model/optimizer fields of the benchmark configurations: "A" (8L d512, CPU-runnable) and "D" (12L d768, 125M)."""
 
     opt = ooptim.OptimizerConfig(learning_rate=2.0 ** -8, steps=steps, warmup_steps=warmup_steps(steps, 0.1))
     if name == "A":
