@@ -13,7 +13,8 @@
 //            K1  recompute logits^T, write G^T = bf16((exp(logit-lse) - onehot)*ct)
 //                as [chunk, n] (zero for rows >= semantic vocab);
 //            K2  dW[chunk] += G^T h     (split over tokens, fp32 atomics);
-//            K3  dh_acc    += G W[chunk] (fp32), rounded to bf16 at the end.
+//            K3  dh_acc    += G W[chunk] (fp32 atomics, split over the chunk),
+//                rounded to bf16 at the end.
 #include "gemm_core.h"
 
 #include <math.h>
@@ -201,7 +202,40 @@ __global__ void zero_f32_kernel(float* __restrict__ x, int64_t n) {
 inline unsigned tiles_of(int M, int N) { return (unsigned)(ceil_div(M, BM) * ceil_div(N, BN)); }
 
 constexpr int kDefaultChunk = 8192;
-constexpr int kDwSplit = 4;
+
+int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cached[dev] = c;
+  }
+  return cached[dev];
+}
+
+// K-split count for a GEMM of `tiles` output tiles over k_iters BK-steps.
+// One 256x256 workgroup fills a CU (its LDS use allows no second), so the grid
+// runs in ceil(tiles*split/CUs) rounds of k_iters/split steps each, plus one
+// fp32 atomic epilogue per round (about 3% of a full-K mainloop).  The split
+// minimising that estimate keeps the last round from running a CU-sized
+// grid a quarter full, which a fixed split does for skinny outputs.
+int choose_split(unsigned tiles, int k_iters) {
+  const int cus = device_cus();
+  const int max_split = k_iters / 4 > 1 ? k_iters / 4 : 1;
+  double best = 1e30;
+  int best_split = 1;
+  for (int s = 1; s <= max_split && s <= 256; ++s) {
+    const double rounds = (double)ceil_div((int64_t)tiles * s, (int64_t)cus);
+    const double cost = rounds * (1.0 / s + 0.03);
+    if (cost < best * 0.999) {
+      best = cost;
+      best_split = s;
+    }
+  }
+  return best_split;
+}
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -271,6 +305,11 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
     GPTRIG_CHECK_LAUNCH();
   }
+  {
+    const int64_t total = (int64_t)n * d;
+    zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, total);
+    GPTRIG_CHECK_LAUNCH();
+  }
   for (int v0 = 0; v0 < vocab; v0 += chunk) {
     const int vc = vocab - v0 < chunk ? vocab - v0 : chunk;
     Operand Wc{Wp + (size_t)v0 * d, d}, Hd{Hp, d};
@@ -279,13 +318,15 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     GPTRIG_CHECK_LAUNCH();
     // dW[v0:v0+vc] += G^T h : A = G^T [vc][n] (K-major), B = h [n][d] (MN-major); split over tokens.
     Operand Ag{gt, n}, Bh{Hp, d};
-    gemm_f32_kernel<true, false><<<tiles_of(vc, d) * kDwSplit, gemm::THREADS, 0, s>>>(
-        Ag, Bh, vc, d, n, kDwSplit, dweight + (size_t)v0 * d, d, 2);
+    const int dw_split = choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
+    gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(
+        Ag, Bh, vc, d, n, dw_split, dweight + (size_t)v0 * d, d, 2);
     GPTRIG_CHECK_LAUNCH();
     // dh += G W[v0:v0+vc] : A(m=n, k=v) = G^T [vc][n] (MN-major), B(k=v, n=j) = W [vc][d] (MN-major).
     Operand Agt{gt, n}, Bw{Wp + (size_t)v0 * d, d};
-    gemm_f32_kernel<false, false><<<tiles_of(n, d), gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, 1, dh_acc, d,
-                                                                             v0 > 0 ? 1 : 0);
+    const int dh_split = choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
+    gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
+                                                                                        dh_acc, d, 2);
     GPTRIG_CHECK_LAUNCH();
   }
   const int64_t total = (int64_t)n * d;
@@ -302,11 +343,7 @@ int gptrig_weight_grad(const void* x, const void* dy, float* dw, int n, int rows
   if (n <= 0 || rows_in <= 0 || cols_out <= 0 || rows_in % 8 || cols_out % 8) return GPTRIG_E_SHAPE;
   if (((uintptr_t)x | (uintptr_t)dy) & 15) return GPTRIG_E_SHAPE;
   const unsigned tiles = tiles_of(rows_in, cols_out);
-  // About 1.5 workgroups per CU: enough to fill the GPU, few fp32 atomics.
-  int split = (int)((384 + tiles - 1) / tiles);
-  const int max_split = ceil_div(n, 2 * gemm::BK);
-  if (split > max_split) split = max_split;
-  if (split < 1) split = 1;
+  const int split = choose_split(tiles, ceil_div(n, gemm::BK));
   // A(m = i, k = t) = X[t][i] (MN-major), B(k = t, n = j) = dY[t][j] (MN-major).
   Operand A{(const bf16*)x, rows_in}, B{(const bf16*)dy, cols_out};
   gemm_f32_kernel<false, false><<<tiles * split, gemm::THREADS, 0, (hipStream_t)stream>>>(A, B, rows_in, cols_out, n,
