@@ -143,10 +143,14 @@ __global__ void __launch_bounds__(gemm::THREADS)
 
 // C (fp32, row-major [M][ldc]) = / += / atomic+= A B over K range of this split.
 // mode 0: store, 1: accumulate (read-modify-write), 2: atomic add.
+// colsum (nullable, MN-major B only): colsum[n] atomic+= sum over this split's
+// K range of B(k, n), computed by the workgroups of the first M tile from the
+// B slabs already in LDS (the bias gradient of a linear layer, fused into
+// its weight gradient).
 template <bool AK, bool BKM>
 __global__ void __launch_bounds__(gemm::THREADS)
     gemm_f32_kernel(Operand A, Operand B, int M, int N, int K, int ksplit, float* __restrict__ C, int64_t ldc,
-                    int mode) {
+                    int mode, float* __restrict__ colsum) {
   __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int split = blockIdx.x / tiles;
@@ -155,10 +159,28 @@ __global__ void __launch_bounds__(gemm::THREADS)
   const int kslice = ((K + ksplit - 1) / ksplit + gemm::BK - 1) / gemm::BK * gemm::BK;
   const int k_begin = split * kslice;
   const int k_end = min(K, k_begin + kslice);
-  f32x16 acc[4][2];
-  gemm::mainloop<AK, BKM>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, lds);
-  if (k_begin >= k_end) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  f32x16 acc[4][2];
+  f32x4 csum = f32x4{};
+  const bool do_colsum = !BKM && colsum != nullptr && tm == 0;
+  gemm::mainloop<AK, BKM, !BKM>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, lds, &csum, do_colsum);
+  if (k_begin >= k_end) return;
+  if (do_colsum) {
+    // Reduce the 8 row groups of each column through LDS (the mainloop ended
+    // with a barrier, so the slabs are free).
+    float* red = reinterpret_cast<float*>(lds);
+    const int n4 = (tid & 63) * 4, grp = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[grp * 256 + n4 + j] = csum[j];
+    __syncthreads();
+    if (tid < 256) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) t += red[g * 256 + tid];
+      const int n = tn * BN + tid;
+      if (n < N) atomicAdd(colsum + n, t);
+    }
+  }
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
@@ -320,13 +342,13 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     Operand Ag{gt, n}, Bh{Hp, d};
     const int dw_split = choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
     gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(
-        Ag, Bh, vc, d, n, dw_split, dweight + (size_t)v0 * d, d, 2);
+        Ag, Bh, vc, d, n, dw_split, dweight + (size_t)v0 * d, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
     // dh += G W[v0:v0+vc] : A(m=n, k=v) = G^T [vc][n] (MN-major), B(k=v, n=j) = W [vc][d] (MN-major).
     Operand Agt{gt, n}, Bw{Wp + (size_t)v0 * d, d};
     const int dh_split = choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
     gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
-                                                                                        dh_acc, d, 2);
+                                                                                        dh_acc, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
   }
   const int64_t total = (int64_t)n * d;
@@ -335,10 +357,13 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
   return GPTRIG_OK;
 }
 
-// dW (f32 [rows_in, cols_out], += ) = X^T dY for X bf16 [n, rows_in], dY bf16 [n, cols_out]:
-// the weight gradient of rig/nn.py:55-56 (linear), split over the n tokens
-// with fp32 atomics so the skinny [d_in, d_out] output still fills the GPU.
-int gptrig_weight_grad(const void* x, const void* dy, float* dw, int n, int rows_in, int cols_out, void* stream) {
+// dW (f32 [rows_in, cols_out], += ) = X^T dY for X bf16 [n, rows_in], dY bf16 [n, cols_out],
+// and (db nullable) db (f32 [cols_out], += ) = column sums of dY: the weight and
+// bias gradients of rig/nn.py:55-56 (linear).  Split over the n tokens with
+// fp32 atomics so the skinny [d_in, d_out] output still fills the GPU; the
+// bias sums come from the dY slabs the GEMM already stages in LDS.
+int gptrig_weight_grad(const void* x, const void* dy, float* dw, float* db, int n, int rows_in, int cols_out,
+                       void* stream) {
   if (!x || !dy || !dw) return GPTRIG_E_NULL;
   if (n <= 0 || rows_in <= 0 || cols_out <= 0 || rows_in % 8 || cols_out % 8) return GPTRIG_E_SHAPE;
   if (((uintptr_t)x | (uintptr_t)dy) & 15) return GPTRIG_E_SHAPE;
@@ -347,7 +372,7 @@ int gptrig_weight_grad(const void* x, const void* dy, float* dw, int n, int rows
   // A(m = i, k = t) = X[t][i] (MN-major), B(k = t, n = j) = dY[t][j] (MN-major).
   Operand A{(const bf16*)x, rows_in}, B{(const bf16*)dy, cols_out};
   gemm_f32_kernel<false, false><<<tiles * split, gemm::THREADS, 0, (hipStream_t)stream>>>(A, B, rows_in, cols_out, n,
-                                                                                         split, dw, cols_out, 2);
+                                                                                         split, dw, cols_out, 2, db);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

@@ -115,11 +115,29 @@ __device__ __forceinline__ void tile_coords(int pid, int M, int N, int& tm, int&
   tn = (pid % in_group) / gsize;
 }
 
+// Column sums of an MN-major B slab: thread t adds rows 8(t/64) .. +7 of
+// columns 4(t%64) .. +3 (one 8-byte LDS read per row) into sum.
+__device__ __forceinline__ void colsum_slab(f32x4& sum, const lds_t* lb, int tid) {
+  const int n4 = (tid & 63) * 4, k0 = (tid >> 6) * 8;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const bf16x4 v = *(const __attribute__((address_space(3))) bf16x4*)(lb + (k0 + k) * MLD + n4);
+    sum[0] += (float)v[0];
+    sum[1] += (float)v[1];
+    sum[2] += (float)v[2];
+    sum[3] += (float)v[3];
+  }
+}
+
 // acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
 // with wm0 = 128*(wave&1), wn0 = 64*(wave>>1); K range [k_begin, k_end).
-template <bool AK, bool BKM>
+// With kColSum (MN-major B only) and colsum_on, colsum also accumulates the
+// column sums of B over the K range (see colsum_slab for the thread mapping).
+template <bool AK, bool BKM, bool kColSum = false>
 __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
-                                         int k_end, int tm0, int tn0, bf16* lds) {
+                                         int k_end, int tm0, int tn0, bf16* lds, f32x4* colsum = nullptr,
+                                         bool colsum_on = false) {
+  static_assert(!kColSum || !BKM, "column sums need an MN-major B operand");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = 128 * (wave & 1), wn0 = 64 * (wave >> 1);
 #pragma unroll
@@ -155,6 +173,7 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(fa[mb], fb[nb], acc[mb][nb]);
     }
+    if (kColSum && colsum_on) colsum_slab(*colsum, lb, tid);
     if (kt + 1 < nk) {
       store_slab<AK>(lbase + (buf ^ 1) * SLAB, sa, tid);
       store_slab<BKM>(lbase + (2 + (buf ^ 1)) * SLAB, sb, tid);

@@ -324,10 +324,8 @@ class GPTTrainer:
 
         A = self.arena
         n, rows_in = inp.shape
-        _lib.call("gptrig_weight_grad", inp.data_ptr(), dout.data_ptr(), A.grad(prefix + "_w").data_ptr(), n, rows_in,
-                  dout.shape[1], _lib.stream())
-        _lib.call("gptrig_bias_grad", dout.data_ptr(), dout.shape[0], dout.shape[1], A.grad(prefix + "_b").data_ptr(),
-                  _lib.stream())
+        _lib.call("gptrig_weight_grad", inp.data_ptr(), dout.data_ptr(), A.grad(prefix + "_w").data_ptr(),
+                  A.grad(prefix + "_b").data_ptr(), n, rows_in, dout.shape[1], _lib.stream())
 
     # -- the step ----------------------------------------------------------------------
     def train_step(self, x: torch.Tensor, y: torch.Tensor) -> None:

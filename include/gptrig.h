@@ -102,10 +102,13 @@ int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const f
                        void* dx, float* dscale, int accumulate_dscale, void* workspace, size_t workspace_bytes,
                        int rows, int d, void* stream);
 
-/* Weight gradient of rig/nn.py:55-56 (linear, y = x W + b): dw f32 [rows_in,
- * cols_out] += x^T dy for x bf16 [n, rows_in], dy bf16 [n, cols_out]
- * (rows_in, cols_out multiples of 8).  Accumulates with fp32 atomics. */
-int gptrig_weight_grad(const void* x, const void* dy, float* dw, int n, int rows_in, int cols_out, void* stream);
+/* Weight and bias gradients of rig/nn.py:55-56 (linear, y = x W + b):
+ * dw f32 [rows_in, cols_out] += x^T dy for x bf16 [n, rows_in], dy bf16
+ * [n, cols_out] (rows_in, cols_out multiples of 8), and, when db is not NULL,
+ * db f32 [cols_out] += column sums of dy in the same pass.  Accumulates with
+ * fp32 atomics. */
+int gptrig_weight_grad(const void* x, const void* dy, float* dw, float* db, int n, int rows_in, int cols_out,
+                       void* stream);
 
 /* Bias gradient of rig/nn.py:55-56 (linear): db f32 [cols] += sum over rows of
  * dy bf16 [rows, cols] (cols % 8 == 0). */

@@ -227,7 +227,7 @@ def train_step(state: TrainState, x: torch.Tensor, y: torch.Tensor, config: Conf
     lr, gnorm = ooptim.adamw_step(state.params, grads, state.m, state.v, state.step, config.optimizer,
                                   config.parameterization, config.width_multiplier, config.depth_multiplier,
                                   config.depth_alpha)
-    record = {"loss": float(loss), "learning_rate": lr, "grad_norm": gnorm}
+    record = {"loss": float(loss.detach()), "learning_rate": lr, "grad_norm": gnorm}
     state.history.append((record["loss"], lr, gnorm))
     return record
 

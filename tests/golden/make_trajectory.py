@@ -1,0 +1,56 @@
+"""Write the config-A 20-step training trajectory of the CPU oracle.
+
+Config A (the reference's CPU-runnable GPT step): 8 layers, d_model 512,
+8 heads x 64, RoPE, pre-norm, GELU MLP 4x, vocab 50304, seq 1024, batch 8,
+bf16 compute with fp32 AdamW master weights (base LR 2^-8, warmup 10% of 20
+steps, cosine), init std 0.02 from seed 0, tokens uniform int32 from numpy
+``default_rng(0)`` windows ``[20, 8, 1025]`` (x = w[:, :-1], y = w[:, 1:]).
+
+Usage: ``python tests/golden/make_trajectory.py`` (about 10 minutes on 8
+cores).  Output: ``tests/golden/config_a_trajectory.json`` with one
+(loss, learning_rate, grad_norm) row per step.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+import torch  # noqa: E402
+
+from oracle import model as om  # noqa: E402
+
+STEPS = 20
+SEED = 0
+
+
+def main() -> None:
+    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
+    config = om.baseline_config("A", steps=STEPS)
+    windows = om.synthetic_windows(SEED, STEPS, config.batch_size, config.seq_len, config.vocab_size)
+    state = om.init_state(config, SEED)
+    rows = []
+    for i in range(STEPS):
+        t0 = time.time()
+        w = torch.from_numpy(windows[i])
+        rec = om.train_step(state, w[:, :-1], w[:, 1:], config)
+        rows.append([rec["loss"], rec["learning_rate"], rec["grad_norm"]])
+        print(f"step {i + 1}: {rows[-1]} ({time.time() - t0:.1f} s)", flush=True)
+    out = {
+        "config": "A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup 2 cosine, 20 steps",
+        "seed": SEED,
+        "windows": "numpy default_rng(0).integers(0, 50304, (20, 8, 1025), int32)",
+        "columns": ["loss", "learning_rate", "grad_norm"],
+        "rows": rows,
+    }
+    with open(os.path.join(HERE, "config_a_trajectory.json"), "w") as f:
+        json.dump(out, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()

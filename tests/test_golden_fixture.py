@@ -1,0 +1,42 @@
+"""Checks of the committed config-A trajectory fixture (CPU).
+
+The fixture holds the oracle's 20-step (loss, learning rate, grad norm)
+history; the GPU trajectory test compares against it.  Here its columns are
+checked against what the mathematics fixes independently of the oracle's code:
+the learning-rate column against the closed-form warmup + cosine schedule of
+``recipes/reference/train.py:1219-1236`` (base 2^-8, 2 warmup steps of 20,
+floor 0.1), and the first loss against ln(V) for a near-uniform softmax at
+std-0.02 initialisation.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+
+FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "config_a_trajectory.json")
+
+
+def closed_form_lr(step: int, steps: int = 20, warmup: int = 2, base: float = 2.0 ** -8, floor: float = 0.1):
+    w = min(1.0, step / warmup)
+    progress = min(max((step - warmup) / (steps - warmup), 0.0), 1.0)
+    return base * w * (floor + (1.0 - floor) * 0.5 * (1.0 + math.cos(math.pi * progress)))
+
+
+def test_fixture_shape_and_learning_rate_column():
+    with open(FIXTURE) as f:
+        data = json.load(f)
+    rows = np.asarray(data["rows"], dtype=np.float64)
+    assert rows.shape == (20, 3)
+    want = np.array([closed_form_lr(s) for s in range(1, 21)])
+    np.testing.assert_allclose(rows[:, 1], want, rtol=1e-6)
+    assert np.all(np.isfinite(rows)) and np.all(rows[:, 2] > 0)
+
+
+def test_fixture_first_loss_is_near_uniform():
+    with open(FIXTURE) as f:
+        rows = np.asarray(json.load(f)["rows"], dtype=np.float64)
+    assert abs(rows[0, 0] - math.log(50304)) <= 0.02 * math.log(50304)

@@ -354,15 +354,22 @@ def test_bias_grad_column_sum():
         assert float((db.cpu().double() - want).abs().max()) <= 1e-3
 
 
-def test_weight_grad_split_k_gemm():
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_weight_grad_split_k_gemm(with_bias):
     from gptrig import _lib
 
-    for n, rin, cout in ((4096, 768, 2304), (1000, 64, 200), (8192, 3072, 768)):
+    for n, rin, cout in ((4096, 768, 2304), (1000, 64, 200), (8192, 3072, 768), (32768, 768, 768)):
         x = randn((n, rin), 111)
         dy = randn((n, cout), 112)
         dw = torch.full((rin, cout), 0.25, device=DEV)
+        db = torch.full((cout,), -0.5, device=DEV) if with_bias else None
         xg, dyg = x.to(DEV), dy.to(DEV)  # keep the device copies alive across the call
-        _lib.call("gptrig_weight_grad", xg.data_ptr(), dyg.data_ptr(), dw.data_ptr(), n, rin, cout, _lib.stream())
+        _lib.call("gptrig_weight_grad", xg.data_ptr(), dyg.data_ptr(), dw.data_ptr(),
+                  None if db is None else db.data_ptr(), n, rin, cout, _lib.stream())
         want = x.double().t() @ dy.double() + 0.25
         err = float((dw.cpu().double() - want).abs().max())
         assert err <= 1e-3 * float(want.abs().max()), (n, rin, cout, err)
+        if with_bias:
+            # Fused bias gradient: column sums of dy over all n rows (every split).
+            want_b = dy.double().sum(0) - 0.5
+            assert float((db.cpu().double() - want_b).abs().max()) <= 1e-3 * max(1.0, float(want_b.abs().max()))
