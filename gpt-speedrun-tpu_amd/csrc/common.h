@@ -53,6 +53,24 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// GELU, tanh approximation (jax.nn.gelu(approximate=True)), in fp32.
+__device__ __forceinline__ float tanh_fast(float u) {
+  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-inf.
+  float e = fast_exp2(2.0f * GPTRIG_LOG2E * u);
+  return 1.0f - 2.0f / (e + 1.0f);
+}
+__device__ __forceinline__ float gelu_f(float x) {
+  const float k = 0.7978845608028654f;  // sqrt(2/pi)
+  float u = k * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanh_fast(u));
+}
+__device__ __forceinline__ float gelu_grad_f(float x) {
+  const float k = 0.7978845608028654f;
+  float u = k * (x + 0.044715f * x * x * x);
+  float t = tanh_fast(u);
+  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * 0.044715f * x * x);
+}
+
 // Pack 8 floats into an MFMA bf16 operand.
 __device__ __forceinline__ bf16x8 pack8(const float* v) {
   bf16x8 r;

@@ -194,23 +194,6 @@ __global__ void __launch_bounds__(256) bias_grad_kernel(const bf16* __restrict__
 // ----------------------------------------------------------------------------
 // GELU, tanh approximation (jax.nn.gelu(approximate=True), train.py:1171)
 // ----------------------------------------------------------------------------
-__device__ __forceinline__ float tanh_fast(float u) {
-  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-inf.
-  float e = fast_exp2(2.0f * GPTRIG_LOG2E * u);
-  return 1.0f - 2.0f / (e + 1.0f);
-}
-__device__ __forceinline__ float gelu_f(float x) {
-  const float k = 0.7978845608028654f;  // sqrt(2/pi)
-  float u = k * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanh_fast(u));
-}
-__device__ __forceinline__ float gelu_grad_f(float x) {
-  const float k = 0.7978845608028654f;
-  float u = k * (x + 0.044715f * x * x * x);
-  float t = tanh_fast(u);
-  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * 0.044715f * x * x);
-}
-
 __global__ void gelu_fwd_kernel(const bf16* __restrict__ x, bf16* __restrict__ y, int64_t n) {
   int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (i + 8 <= n) {

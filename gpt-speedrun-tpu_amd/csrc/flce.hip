@@ -225,40 +225,6 @@ inline unsigned tiles_of(int M, int N) { return (unsigned)(ceil_div(M, BM) * cei
 
 constexpr int kDefaultChunk = 8192;
 
-int device_cus() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-    cached[dev] = c;
-  }
-  return cached[dev];
-}
-
-// K-split count for a GEMM of `tiles` output tiles over k_iters BK-steps.
-// One 256x256 workgroup fills a CU (its LDS use allows no second), so the grid
-// runs in ceil(tiles*split/CUs) rounds of k_iters/split steps each, plus one
-// fp32 atomic epilogue per round (about 3% of a full-K mainloop).  The split
-// minimising that estimate keeps the last round from running a CU-sized
-// grid a quarter full, which a fixed split does for skinny outputs.
-int choose_split(unsigned tiles, int k_iters) {
-  const int cus = device_cus();
-  const int max_split = k_iters / 4 > 1 ? k_iters / 4 : 1;
-  double best = 1e30;
-  int best_split = 1;
-  for (int s = 1; s <= max_split && s <= 256; ++s) {
-    const double rounds = (double)ceil_div((int64_t)tiles * s, (int64_t)cus);
-    const double cost = rounds * (1.0 / s + 0.03);
-    if (cost < best * 0.999) {
-      best = cost;
-      best_split = s;
-    }
-  }
-  return best_split;
-}
-
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int resolve_chunk(int vocab, int vocab_chunk) {
@@ -340,13 +306,13 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     GPTRIG_CHECK_LAUNCH();
     // dW[v0:v0+vc] += G^T h : A = G^T [vc][n] (K-major), B = h [n][d] (MN-major); split over tokens.
     Operand Ag{gt, n}, Bh{Hp, d};
-    const int dw_split = choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
+    const int dw_split = gemm::choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
     gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(
         Ag, Bh, vc, d, n, dw_split, dweight + (size_t)v0 * d, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
     // dh += G W[v0:v0+vc] : A(m=n, k=v) = G^T [vc][n] (MN-major), B(k=v, n=j) = W [vc][d] (MN-major).
     Operand Agt{gt, n}, Bw{Wp + (size_t)v0 * d, d};
-    const int dh_split = choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
+    const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
     gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
                                                                                         dh_acc, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
@@ -368,7 +334,7 @@ int gptrig_weight_grad(const void* x, const void* dy, float* dw, float* db, int 
   if (n <= 0 || rows_in <= 0 || cols_out <= 0 || rows_in % 8 || cols_out % 8) return GPTRIG_E_SHAPE;
   if (((uintptr_t)x | (uintptr_t)dy) & 15) return GPTRIG_E_SHAPE;
   const unsigned tiles = tiles_of(rows_in, cols_out);
-  const int split = choose_split(tiles, ceil_div(n, gemm::BK));
+  const int split = gemm::choose_split(tiles, ceil_div(n, gemm::BK));
   // A(m = i, k = t) = X[t][i] (MN-major), B(k = t, n = j) = dY[t][j] (MN-major).
   Operand A{(const bf16*)x, rows_in}, B{(const bf16*)dy, cols_out};
   gemm_f32_kernel<false, false><<<tiles * split, gemm::THREADS, 0, (hipStream_t)stream>>>(A, B, rows_in, cols_out, n,

@@ -34,9 +34,14 @@ typedef __attribute__((address_space(3))) bf16x8 lds_x8;
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 typedef const __attribute__((address_space(1))) bf16x8 gbl_x8;
 
+// Element (row r, column c) of the stored matrix is p[row(r) * ld + c] with
+// row(r) = idx ? idx[r] : r: idx gathers rows (K-major: M/N rows; MN-major:
+// k rows), which is how the routed expert GEMMs read token rows in bucket
+// order without a gathered copy.
 struct Operand {
   const bf16* p;
   int64_t ld;
+  const int32_t* idx = nullptr;
 };
 
 __device__ __forceinline__ lds_t* lds_cast(bf16* p) { return (lds_t*)p; }
@@ -55,11 +60,21 @@ __device__ __forceinline__ void load_slab(bf16x8 (&st)[4], Operand op, int mn0, 
     if (KMAJOR) {
       const int row = idx >> 3, kc = (idx & 7) * 8;
       const int m = mn0 + row, k = k0 + kc;
-      st[r] = (m < MN && k < K) ? *(gbl_x8*)(op.p + (int64_t)m * op.ld + k) : bf16x8{};
+      if (m < MN && k < K) {
+        const int64_t pr = op.idx ? op.idx[m] : m;
+        st[r] = *(gbl_x8*)(op.p + pr * op.ld + k);
+      } else {
+        st[r] = bf16x8{};
+      }
     } else {
       const int kk = idx >> 5, mc = (idx & 31) * 8;
       const int m = mn0 + mc, k = k0 + kk;
-      st[r] = (m < MN && k < K) ? *(gbl_x8*)(op.p + (int64_t)k * op.ld + m) : bf16x8{};
+      if (m < MN && k < K) {
+        const int64_t pk = op.idx ? op.idx[k] : k;
+        st[r] = *(gbl_x8*)(op.p + pk * op.ld + m);
+      } else {
+        st[r] = bf16x8{};
+      }
     }
   }
 }
@@ -180,6 +195,42 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand
     }
     __syncthreads();
   }
+}
+
+// ---- host side: launch shaping ----
+
+inline int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cached[dev] = c;
+  }
+  return cached[dev];
+}
+
+// K-split count for a GEMM of `tiles` output tiles over k_iters BK-steps.
+// One 256x256 workgroup fills a CU (its LDS use allows no second), so the grid
+// runs in ceil(tiles*split/CUs) rounds of k_iters/split steps each, plus one
+// fp32 atomic epilogue per round (about 3% of a full-K mainloop).  The split
+// minimising that estimate keeps the last round from running a CU-sized
+// grid a quarter full, which a fixed split does for skinny outputs.
+inline int choose_split(unsigned tiles, int k_iters) {
+  const int cus = device_cus();
+  const int max_split = k_iters / 4 > 1 ? k_iters / 4 : 1;
+  double best = 1e30;
+  int best_split = 1;
+  for (int s = 1; s <= max_split && s <= 256; ++s) {
+    const double rounds = (double)ceil_div((int64_t)tiles * s, (int64_t)cus);
+    const double cost = rounds * (1.0 / s + 0.03);
+    if (cost < best * 0.999) {
+      best = cost;
+      best_split = s;
+    }
+  }
+  return best_split;
 }
 
 }  // namespace gemm

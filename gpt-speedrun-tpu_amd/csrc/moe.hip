@@ -6,8 +6,21 @@
 // route_sort: one 1024-thread workgroup builds the dropless bucket layout:
 //   counts[e], and order = stable argsort(chosen.reshape(-1)) by counting sort
 //   (per-expert bases from an exclusive scan of counts, stable ranks from
-//   wave ballots in slot order), rows = order / top_k.
+//   wave ballots in slot order), rows = order / top_k, position = order^-1.
+//
+// The routed MLP around it (:1275-1293):
+//   router_logits   fp32 x @ router_w (one wave per token, weights in LDS);
+//   moe_gmm         grouped GEMM over the expert buckets on the MFMA GEMM core:
+//                   A rows gathered through `rows` (no gathered copy), epilogue
+//                   bias (+ GELU, or x GELU' for the backward);
+//   moe_combine     combined[t] = sum over the token's slots, in bucket order,
+//                   of bf16(out * bf16(gate)) -- the .at[rows].add rounding;
+//   moe_stats       mean probability, load, (entropy, top-1 gate, logit RMS);
+// and their backward: combine_bwd, moe_gmm_dw (per-expert weight + bias
+// gradients, split-K fp32 atomics), gather_bwd (the VJP of flat[rows]) and
+// router_bwd (gate/probability softmax VJPs, dx and d router_w).
 #include "common.h"
+#include "gemm_core.h"
 
 #include <math.h>
 
@@ -58,7 +71,8 @@ __global__ void route_topk_kernel(const float* __restrict__ logits, float* __res
 
 __global__ void __launch_bounds__(1024) route_sort_kernel(const int32_t* __restrict__ chosen, int n_slots, int E,
                                                           int k, int32_t* __restrict__ counts,
-                                                          int32_t* __restrict__ order, int32_t* __restrict__ rows) {
+                                                          int32_t* __restrict__ order, int32_t* __restrict__ rows,
+                                                          int32_t* __restrict__ position) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int base[kMaxExperts];
   __shared__ int wave_cnt[16][kMaxExperts];
@@ -93,6 +107,7 @@ __global__ void __launch_bounds__(1024) route_sort_kernel(const int32_t* __restr
       const int pos = base[my_e] + before + rank;
       order[pos] = s;
       rows[pos] = s / k;
+      if (position) position[s] = pos;
     }
     __syncthreads();
     if (tid < E) {
@@ -102,6 +117,380 @@ __global__ void __launch_bounds__(1024) route_sort_kernel(const int32_t* __restr
     }
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------------------
+// Router logits (:1259-1264): logits[t][e] = sum_d f32(x[t][d]) * w[d][e].
+// Each wave owns kRouterTokens consecutive tokens; lane l holds d = l + 64i.
+// ---------------------------------------------------------------------------
+constexpr int kMaxRouterExperts = 16;
+constexpr int kRouterTokens = 16;
+constexpr int kMaxRouterWidth = 4096;
+
+__global__ void __launch_bounds__(256) router_logits_kernel(const bf16* __restrict__ x, const float* __restrict__ w,
+                                                            float* __restrict__ logits, int T, int D, int E) {
+  extern __shared__ float wsh[];  // [D][E]
+  for (int i = threadIdx.x; i < D * E; i += blockDim.x) wsh[i] = w[i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = (blockIdx.x * 4 + wave) * kRouterTokens;
+  for (int tt = 0; tt < kRouterTokens; ++tt) {
+    const int t = t0 + tt;
+    if (t >= T) break;
+    float acc[kMaxRouterExperts];
+#pragma unroll
+    for (int e = 0; e < kMaxRouterExperts; ++e) acc[e] = 0.f;
+    for (int d = lane; d < D; d += 64) {
+      const float xv = (float)x[(size_t)t * D + d];
+#pragma unroll
+      for (int e = 0; e < kMaxRouterExperts; ++e)
+        if (e < E) acc[e] = fmaf(xv, wsh[d * E + e], acc[e]);
+    }
+    float mine = 0.f;
+#pragma unroll
+    for (int e = 0; e < kMaxRouterExperts; ++e) {
+      if (e < E) {
+        const float v = wave_sum(acc[e]);
+        if (lane == e) mine = v;
+      }
+    }
+    if (lane < E) logits[(size_t)t * E + lane] = mine;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM over the expert buckets (megablox.gmm contract):
+//   out[off_e + r][n] = sum_k A[off_e + r][k] * B_e(k, n),  r < counts[e],
+// A K-major [R][K] (row i read from a_idx ? a_idx[i] : i), B_e either [K][N]
+// (kBT = false: rhs + e*K*N) or [N][K] (kBT = true: the transpose, for dX).
+// Grid: (ceil(R/256) + E) M-tile slots x ceil(N/256); surplus slots exit.
+// kMode 0: out = bf16(acc) (+ bias)
+//       1: pre = bf16(bf16(acc) + bias), out = bf16(gelu(pre))
+//       2: out = bf16(bf16(acc) * gelu'(pre))   (pre read, same layout as out)
+// ---------------------------------------------------------------------------
+template <bool kBT, int kMode>
+__global__ void __launch_bounds__(gemm::THREADS)
+    moe_gmm_kernel(const bf16* __restrict__ lhs, const int32_t* __restrict__ a_idx, int64_t lda,
+                   const bf16* __restrict__ rhs, const int32_t* __restrict__ counts, int E, int K, int N,
+                   const bf16* __restrict__ bias, bf16* __restrict__ out, bf16* __restrict__ pre, int64_t ldo) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
+  const int ntn = (N + gemm::BN - 1) / gemm::BN;
+  const int tn = blockIdx.x % ntn;
+  int tm = blockIdx.x / ntn;
+  int e = 0, off = 0;
+  for (; e < E; ++e) {
+    const int c = counts[e];
+    const int nt = (c + gemm::BM - 1) / gemm::BM;
+    if (tm < nt) break;
+    tm -= nt;
+    off += c;
+  }
+  if (e >= E) return;  // uniform: surplus slot
+  const int cnt = counts[e];
+  gemm::Operand A{a_idx ? lhs : lhs + (int64_t)off * lda, lda, a_idx ? a_idx + off : nullptr};
+  gemm::Operand B = kBT ? gemm::Operand{rhs + (int64_t)e * N * K, K} : gemm::Operand{rhs + (int64_t)e * K * N, N};
+  f32x16 acc[4][2];
+  gemm::mainloop<true, kBT>(acc, A, B, cnt, N, 0, K, tm * gemm::BM, tn * gemm::BN, lds);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int wm = wave & 1, wn = wave >> 1;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int n = tn * gemm::BN + 64 * wn + 32 * nb + l32;
+    if (n >= N) continue;
+    const float bv = bias ? (float)bias[(int64_t)e * N + n] : 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = tm * gemm::BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (m >= cnt) continue;
+        const int64_t o = (int64_t)(off + m) * ldo + n;
+        const float g = (float)(bf16)acc[mb][nb][i];
+        if (kMode == 0) {
+          out[o] = bias ? (bf16)(g + bv) : (bf16)g;
+        } else if (kMode == 1) {
+          const bf16 h = (bf16)(g + bv);
+          pre[o] = h;
+          out[o] = (bf16)gelu_f((float)h);
+        } else {
+          out[o] = (bf16)(g * gelu_grad_f((float)pre[o]));
+        }
+      }
+  }
+}
+
+// Per-expert weight (+ bias) gradients:
+//   dw[e] (f32 [K][N]) += sum_{r in bucket e} A[r][k] * dy[r][n],
+//   db[e] (f32 [N])    += sum_{r in bucket e} dy[r][n]          (nullable),
+// A [R][K] rows read through a_idx (nullable), dy [R][N].  Grid:
+// E x tiles(K, N) x split; bucket e's rows are split into `split` slices.
+__global__ void __launch_bounds__(gemm::THREADS)
+    moe_gmm_dw_kernel(const bf16* __restrict__ lhs, const int32_t* __restrict__ a_idx, int64_t lda,
+                      const bf16* __restrict__ dy, int64_t ldy, const int32_t* __restrict__ counts, int E, int K,
+                      int N, int split, float* __restrict__ dw, float* __restrict__ db) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
+  const int tiles = ((K + gemm::BM - 1) / gemm::BM) * ((N + gemm::BN - 1) / gemm::BN);
+  const int e = blockIdx.x / (tiles * split);
+  const int rem = blockIdx.x % (tiles * split);
+  const int sp = rem / tiles;
+  int tm, tn;
+  gemm::tile_coords(rem % tiles, K, N, tm, tn);
+  int off = 0;
+  for (int i = 0; i < e; ++i) off += counts[i];
+  const int cnt = counts[e];
+  const int kslice = ((cnt + split - 1) / split + gemm::BK - 1) / gemm::BK * gemm::BK;
+  const int k_begin = sp * kslice;
+  const int k_end = min(cnt, k_begin + kslice);
+  if (k_begin >= k_end) return;  // uniform
+  // A(m = k-index, k = bucket row) MN-major; B(k = bucket row, n) MN-major.
+  gemm::Operand A{a_idx ? lhs : lhs + (int64_t)off * lda, lda, a_idx ? a_idx + off : nullptr};
+  gemm::Operand B{dy + (int64_t)off * ldy, ldy};
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  f32x16 acc[4][2];
+  f32x4 csum = f32x4{};
+  const bool do_colsum = db != nullptr && tm == 0;
+  gemm::mainloop<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, lds, &csum,
+                                     do_colsum);
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int wm = wave & 1, wn = wave >> 1;
+  float* dwe = dw + (int64_t)e * K * N;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int n = tn * gemm::BN + 64 * wn + 32 * nb + l32;
+    if (n >= N) continue;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = tm * gemm::BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (m < K) atomicAdd(dwe + (int64_t)m * N + n, acc[mb][nb][i]);
+      }
+  }
+  if (do_colsum) {
+    float* red = reinterpret_cast<float*>(lds);
+    const int n4 = (tid & 63) * 4, grp = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[grp * 256 + n4 + j] = csum[j];
+    __syncthreads();
+    if (tid < 256) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) t += red[g * 256 + tid];
+      const int n = tn * gemm::BN + tid;
+      if (n < N) atomicAdd(db + (int64_t)e * N + n, t);
+    }
+  }
+}
+
+// Sort the (at most kMaxTopK) bucket positions of one token ascending.
+constexpr int kMaxTopK = 8;
+__device__ __forceinline__ void token_slots(const int32_t* __restrict__ position, const float* __restrict__ gate,
+                                            int t, int k, int (&p)[kMaxTopK], float (&g)[kMaxTopK]) {
+  for (int j = 0; j < k; ++j) {
+    p[j] = position[(size_t)t * k + j];
+    g[j] = gate ? (float)(bf16)gate[(size_t)t * k + j] : 0.f;
+  }
+  for (int a = 1; a < k; ++a)
+    for (int b = a; b > 0 && p[b - 1] > p[b]; --b) {
+      const int tp = p[b];
+      p[b] = p[b - 1];
+      p[b - 1] = tp;
+      const float tg = g[b];
+      g[b] = g[b - 1];
+      g[b - 1] = tg;
+    }
+}
+
+// combined[t] = bf16 sum, in bucket order, of bf16(out[p] * bf16(gate)):
+// weighted = out * gate[order].astype(bf16); zeros.at[rows].add(weighted).
+__global__ void __launch_bounds__(256) moe_combine_kernel(const bf16* __restrict__ out, const int32_t* __restrict__ position,
+                                                          const float* __restrict__ gate, bf16* __restrict__ combined,
+                                                          int T, int D, int k) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  int p[kMaxTopK];
+  float g[kMaxTopK];
+  token_slots(position, gate, t, k, p, g);
+  for (int c = lane * 4; c < D; c += 256) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < k; ++j) {
+      const bf16x4 v = *reinterpret_cast<const bf16x4*>(out + (size_t)p[j] * D + c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = (float)(bf16)(acc[q] + (float)(bf16)((float)v[q] * g[j]));
+    }
+    bf16x4 o = {(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+    *reinterpret_cast<bf16x4*>(combined + (size_t)t * D + c) = o;
+  }
+}
+
+// Backward of the combine: dout[p] = bf16(dcombined[t] * bf16(gate[a])),
+// dgate[a] = sum_n dcombined[t][n] * out[p][n] (fp32), a = t*k + j, p = position[a].
+__global__ void __launch_bounds__(256) moe_combine_bwd_kernel(const bf16* __restrict__ dcombined,
+                                                              const bf16* __restrict__ out,
+                                                              const int32_t* __restrict__ position,
+                                                              const float* __restrict__ gate, bf16* __restrict__ dout,
+                                                              float* __restrict__ dgate, int T, int D, int k) {
+  const int a = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (a >= T * k) return;
+  const int lane = threadIdx.x & 63;
+  const int t = a / k, p = position[a];
+  const float g = (float)(bf16)gate[a];
+  float dot = 0.f;
+  for (int c = lane * 4; c < D; c += 256) {
+    const bf16x4 dc = *reinterpret_cast<const bf16x4*>(dcombined + (size_t)t * D + c);
+    const bf16x4 ov = *reinterpret_cast<const bf16x4*>(out + (size_t)p * D + c);
+    bf16x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o[q] = (bf16)((float)dc[q] * g);
+      dot = fmaf((float)dc[q], (float)ov[q], dot);
+    }
+    *reinterpret_cast<bf16x4*>(dout + (size_t)p * D + c) = o;
+  }
+  dot = wave_sum(dot);
+  if (lane == 0) dgate[a] = dot;
+}
+
+// VJP of grouped = flat[rows]: dx[t] = bf16 sum, in bucket order, of dgrouped[p].
+__global__ void __launch_bounds__(256) moe_gather_bwd_kernel(const bf16* __restrict__ dgrouped,
+                                                             const int32_t* __restrict__ position,
+                                                             bf16* __restrict__ dx, int T, int D, int k) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  int p[kMaxTopK];
+  float g[kMaxTopK];
+  token_slots(position, nullptr, t, k, p, g);
+  for (int c = lane * 4; c < D; c += 256) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < k; ++j) {
+      const bf16x4 v = *reinterpret_cast<const bf16x4*>(dgrouped + (size_t)p[j] * D + c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = (float)(bf16)(acc[q] + (float)v[q]);
+    }
+    bf16x4 o = {(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+    *reinterpret_cast<bf16x4*>(dx + (size_t)t * D + c) = o;
+  }
+}
+
+// Router statistics (:1295-1306), one 1024-thread workgroup:
+// mean_probability[e] = mean_t probs[t][e]; load[e] = counts[e] / (T*k);
+// summary = (mean_t entropy_t, mean_t max_j gate[t][j], sqrt(mean logits^2)).
+__global__ void __launch_bounds__(1024) moe_stats_kernel(const float* __restrict__ logits, const float* __restrict__ probs,
+                                                         const float* __restrict__ gate, const int32_t* __restrict__ counts,
+                                                         int T, int E, int k, float* __restrict__ mean_probability,
+                                                         float* __restrict__ load, float* __restrict__ summary) {
+  __shared__ float red[3 + kMaxExperts][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float pe[kMaxRouterExperts];
+#pragma unroll
+  for (int e = 0; e < kMaxRouterExperts; ++e) pe[e] = 0.f;
+  float ent = 0.f, top = 0.f, sq = 0.f;
+  for (int t = tid; t < T; t += blockDim.x) {
+    float h = 0.f;
+#pragma unroll
+    for (int e = 0; e < kMaxRouterExperts; ++e) {
+      if (e < E) {
+        const float pv = probs[(size_t)t * E + e];
+        const float lv = logits[(size_t)t * E + e];
+        pe[e] += pv;
+        h -= pv * logf(pv + 1.0e-9f);
+        sq = fmaf(lv, lv, sq);
+      }
+    }
+    ent += h;
+    float gm = gate[(size_t)t * k];
+    for (int j = 1; j < k; ++j) gm = fmaxf(gm, gate[(size_t)t * k + j]);
+    top += gm;
+  }
+  float vals[3] = {ent, top, sq};
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const float v = wave_sum(vals[q]);
+    if (lane == 0) red[q][wave] = v;
+  }
+#pragma unroll
+  for (int e = 0; e < kMaxRouterExperts; ++e) {
+    if (e < E) {
+      const float v = wave_sum(pe[e]);
+      if (lane == 0) red[3 + e][wave] = v;
+    }
+  }
+  __syncthreads();
+  if (tid < 3 + E) {
+    float s = 0.f;
+    for (int w = 0; w < 16; ++w) s += red[tid][w];
+    if (tid == 0) summary[0] = s / T;
+    else if (tid == 1) summary[1] = s / T;
+    else if (tid == 2) summary[2] = sqrtf(s / ((float)T * E));
+    else mean_probability[tid - 3] = s / T;
+  }
+  if (tid < E) load[tid] = (float)counts[tid] / (float)((long long)T * k);
+}
+
+// Router backward, per token t (one wave per kRouterTokens tokens):
+//   dchosen[j] = gate[j] * (dgate[j] - sum_i gate[i] dgate[i])        (gate softmax)
+//   dprobs[e]  = dmean_probability[e] / T                              (mean over tokens)
+//   dlogits[e] = probs[e] * (dprobs[e] - sum_i probs[i] dprobs[i]) + sum_{j: chosen[j]=e} dchosen[j]
+//   dx[t][d]   = bf16(dx[t][d] + bf16(sum_e dlogits[e] w[d][e]))       (in place)
+//   dw[d][e]  += sum_t f32(x[t][d]) dlogits[e]                         (fp32 atomics per workgroup)
+__global__ void __launch_bounds__(256) router_bwd_kernel(const bf16* __restrict__ x, const float* __restrict__ w,
+                                                         const float* __restrict__ probs, const int32_t* __restrict__ chosen,
+                                                         const float* __restrict__ gate, const float* __restrict__ dgate,
+                                                         const float* __restrict__ dmean_probability,
+                                                         bf16* __restrict__ dx, float* __restrict__ dw, int T, int D,
+                                                         int E, int k) {
+  extern __shared__ float smem[];
+  float* wsh = smem;           // [D][E]
+  float* dwsh = smem + D * E;  // [D][E] workgroup partial of dw
+  for (int i = threadIdx.x; i < D * E; i += blockDim.x) {
+    wsh[i] = w[i];
+    dwsh[i] = 0.f;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = (blockIdx.x * 4 + wave) * kRouterTokens;
+  for (int tt = 0; tt < kRouterTokens; ++tt) {
+    const int t = t0 + tt;
+    if (t >= T) break;
+    // dlogits for this token, computed redundantly by every lane (E <= 16).
+    float dl[kMaxRouterExperts];
+    float pd = 0.f;
+#pragma unroll
+    for (int e = 0; e < kMaxRouterExperts; ++e) {
+      dl[e] = 0.f;
+      if (e < E && dmean_probability) pd += probs[(size_t)t * E + e] * (dmean_probability[e] / T);
+    }
+#pragma unroll
+    for (int e = 0; e < kMaxRouterExperts; ++e)
+      if (e < E && dmean_probability) dl[e] = probs[(size_t)t * E + e] * (dmean_probability[e] / T - pd);
+    float gd = 0.f;
+    for (int j = 0; j < k; ++j) gd += gate[(size_t)t * k + j] * dgate[(size_t)t * k + j];
+    for (int j = 0; j < k; ++j) {
+      const float dc = gate[(size_t)t * k + j] * (dgate[(size_t)t * k + j] - gd);
+      const int ce = chosen[(size_t)t * k + j];
+#pragma unroll
+      for (int e = 0; e < kMaxRouterExperts; ++e)
+        if (e == ce) dl[e] += dc;
+    }
+    for (int d = lane; d < D; d += 64) {
+      const float xv = (float)x[(size_t)t * D + d];
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < kMaxRouterExperts; ++e) {
+        if (e < E) {
+          s = fmaf(dl[e], wsh[d * E + e], s);
+          atomicAdd(&dwsh[d * E + e], xv * dl[e]);  // LDS atomic: waves of the workgroup share d
+        }
+      }
+      const size_t o = (size_t)t * D + d;
+      dx[o] = (bf16)((float)dx[o] + (float)(bf16)s);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < D * E; i += blockDim.x) atomicAdd(dw + i, dwsh[i]);
 }
 
 }  // namespace
@@ -116,8 +505,8 @@ size_t gptrig_moe_route_workspace_bytes(int tokens, int experts, int top_k) {
 }
 
 int gptrig_moe_route(const float* logits, float* probs, int32_t* chosen, float* gate, int32_t* counts,
-                     int32_t* order, int32_t* rows, void* workspace, size_t workspace_bytes, int tokens, int experts,
-                     int top_k, void* stream) {
+                     int32_t* order, int32_t* rows, int32_t* position, void* workspace, size_t workspace_bytes,
+                     int tokens, int experts, int top_k, void* stream) {
   (void)workspace;
   (void)workspace_bytes;
   if (!logits || !chosen || !gate || !counts || !order || !rows) return GPTRIG_E_NULL;
@@ -126,7 +515,127 @@ int gptrig_moe_route(const float* logits, float* probs, int32_t* chosen, float* 
   hipStream_t s = (hipStream_t)stream;
   route_topk_kernel<<<ceil_div(tokens, 128), 128, 0, s>>>(logits, probs, chosen, gate, tokens, experts, top_k);
   GPTRIG_CHECK_LAUNCH();
-  route_sort_kernel<<<1, 1024, 0, s>>>(chosen, tokens * top_k, experts, top_k, counts, order, rows);
+  route_sort_kernel<<<1, 1024, 0, s>>>(chosen, tokens * top_k, experts, top_k, counts, order, rows, position);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+
+int gptrig_moe_router_logits(const void* x, const float* router_w, float* logits, int tokens, int width, int experts,
+                             void* stream) {
+  if (!x || !router_w || !logits) return GPTRIG_E_NULL;
+  if (tokens <= 0 || width <= 0 || experts <= 0) return GPTRIG_E_SHAPE;
+  if (experts > kMaxRouterExperts || (size_t)width * experts * sizeof(float) > 32768) return GPTRIG_E_UNSUPPORTED;
+  const size_t smem = (size_t)width * experts * sizeof(float);
+  router_logits_kernel<<<ceil_div(tokens, 4 * kRouterTokens), 256, smem, (hipStream_t)stream>>>(
+      (const bf16*)x, router_w, logits, tokens, width, experts);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_gmm(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* rhs, int rhs_transposed,
+                   const int32_t* counts, const void* bias, int mode, void* out, void* pre, int64_t ldo, int rows,
+                   int k, int n, int experts, void* stream) {
+  if (!lhs || !rhs || !counts || !out) return GPTRIG_E_NULL;
+  if ((mode == 1 || mode == 2) && !pre) return GPTRIG_E_NULL;
+  if (rows <= 0 || k <= 0 || n <= 0 || experts <= 0 || mode < 0 || mode > 2) return GPTRIG_E_SHAPE;
+  if (k % 8 || n % 8 || lda % 8 || lda < k || ldo < n) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)lhs | (uintptr_t)rhs) & 15) return GPTRIG_E_SHAPE;
+  if (experts > kMaxExperts) return GPTRIG_E_UNSUPPORTED;
+  const unsigned grid = (unsigned)((ceil_div(rows, gemm::BM) + experts) * ceil_div(n, gemm::BN));
+  hipStream_t s = (hipStream_t)stream;
+  const bf16* L = (const bf16*)lhs;
+  const bf16* Rh = (const bf16*)rhs;
+  const bf16* Bi = (const bf16*)bias;
+  bf16* O = (bf16*)out;
+  bf16* P = (bf16*)pre;
+#define GPTRIG_GMM(BT, MODE)                                                                                     \
+  moe_gmm_kernel<BT, MODE><<<grid, gemm::THREADS, 0, s>>>(L, lhs_rows, lda, Rh, counts, experts, k, n, Bi, O, P, \
+                                                          ldo)
+  if (rhs_transposed) {
+    if (mode == 0) GPTRIG_GMM(true, 0);
+    else if (mode == 1) GPTRIG_GMM(true, 1);
+    else GPTRIG_GMM(true, 2);
+  } else {
+    if (mode == 0) GPTRIG_GMM(false, 0);
+    else if (mode == 1) GPTRIG_GMM(false, 1);
+    else GPTRIG_GMM(false, 2);
+  }
+#undef GPTRIG_GMM
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_gmm_dw(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* dy, int64_t ldy,
+                      const int32_t* counts, float* dw, float* db, int rows, int k, int n, int experts,
+                      void* stream) {
+  if (!lhs || !dy || !counts || !dw) return GPTRIG_E_NULL;
+  if (rows <= 0 || k <= 0 || n <= 0 || experts <= 0) return GPTRIG_E_SHAPE;
+  if (k % 8 || n % 8 || lda % 8 || ldy % 8 || lda < k || ldy < n) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)lhs | (uintptr_t)dy) & 15) return GPTRIG_E_SHAPE;
+  if (experts > kMaxExperts) return GPTRIG_E_UNSUPPORTED;
+  const unsigned tiles = (unsigned)(ceil_div(k, gemm::BM) * ceil_div(n, gemm::BN));
+  const int split = gemm::choose_split(tiles * experts, ceil_div(ceil_div(rows, experts), gemm::BK));
+  moe_gmm_dw_kernel<<<tiles * experts * split, gemm::THREADS, 0, (hipStream_t)stream>>>(
+      (const bf16*)lhs, lhs_rows, lda, (const bf16*)dy, ldy, counts, experts, k, n, split, dw, db);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_combine(const void* out, const int32_t* position, const float* gate, void* combined, int tokens,
+                       int width, int top_k, void* stream) {
+  if (!out || !position || !gate || !combined) return GPTRIG_E_NULL;
+  if (tokens <= 0 || width <= 0 || top_k <= 0 || width % 8) return GPTRIG_E_SHAPE;
+  if (top_k > kMaxTopK) return GPTRIG_E_UNSUPPORTED;
+  moe_combine_kernel<<<ceil_div(tokens, 4), 256, 0, (hipStream_t)stream>>>((const bf16*)out, position, gate,
+                                                                          (bf16*)combined, tokens, width, top_k);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_combine_bwd(const void* dcombined, const void* out, const int32_t* position, const float* gate,
+                           void* dout, float* dgate, int tokens, int width, int top_k, void* stream) {
+  if (!dcombined || !out || !position || !gate || !dout || !dgate) return GPTRIG_E_NULL;
+  if (tokens <= 0 || width <= 0 || top_k <= 0 || width % 8) return GPTRIG_E_SHAPE;
+  if (top_k > kMaxTopK) return GPTRIG_E_UNSUPPORTED;
+  moe_combine_bwd_kernel<<<ceil_div((long long)tokens * top_k, 4), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)dcombined, (const bf16*)out, position, gate, (bf16*)dout, dgate, tokens, width, top_k);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_gather_bwd(const void* dgrouped, const int32_t* position, void* dx, int tokens, int width, int top_k,
+                          void* stream) {
+  if (!dgrouped || !position || !dx) return GPTRIG_E_NULL;
+  if (tokens <= 0 || width <= 0 || top_k <= 0 || width % 8) return GPTRIG_E_SHAPE;
+  if (top_k > kMaxTopK) return GPTRIG_E_UNSUPPORTED;
+  moe_gather_bwd_kernel<<<ceil_div(tokens, 4), 256, 0, (hipStream_t)stream>>>((const bf16*)dgrouped, position,
+                                                                             (bf16*)dx, tokens, width, top_k);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_stats(const float* logits, const float* probs, const float* gate, const int32_t* counts, int tokens,
+                     int experts, int top_k, float* mean_probability, float* load, float* summary, void* stream) {
+  if (!logits || !probs || !gate || !counts || !mean_probability || !load || !summary) return GPTRIG_E_NULL;
+  if (tokens <= 0 || experts <= 0 || top_k <= 0 || top_k > experts) return GPTRIG_E_SHAPE;
+  if (experts > kMaxRouterExperts) return GPTRIG_E_UNSUPPORTED;
+  moe_stats_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(logits, probs, gate, counts, tokens, experts, top_k,
+                                                        mean_probability, load, summary);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_router_bwd(const void* x, const float* router_w, const float* probs, const int32_t* chosen,
+                          const float* gate, const float* dgate, const float* dmean_probability, void* dx,
+                          float* dw_router, int tokens, int width, int experts, int top_k, void* stream) {
+  if (!x || !router_w || !probs || !chosen || !gate || !dgate || !dx || !dw_router) return GPTRIG_E_NULL;
+  if (tokens <= 0 || width <= 0 || experts <= 0 || top_k <= 0 || top_k > experts) return GPTRIG_E_SHAPE;
+  if (experts > kMaxRouterExperts || (size_t)width * experts * sizeof(float) > 32768) return GPTRIG_E_UNSUPPORTED;
+  const size_t smem = 2 * (size_t)width * experts * sizeof(float);
+  router_bwd_kernel<<<ceil_div(tokens, 4 * kRouterTokens), 256, smem, (hipStream_t)stream>>>(
+      (const bf16*)x, router_w, probs, chosen, gate, dgate, dmean_probability, (bf16*)dx, dw_router, tokens, width,
+      experts, top_k);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

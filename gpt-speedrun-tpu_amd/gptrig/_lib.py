@@ -51,7 +51,15 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_weighted_sum": (I, [P, L, F, P, P]),
     "gptrig_fill_f32": (I, [P, L, F, P]),
     "gptrig_moe_route_workspace_bytes": (Z, [I, I, I]),
-    "gptrig_moe_route": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, P]),
+    "gptrig_moe_route": (I, [P, P, P, P, P, P, P, P, P, Z, I, I, I, P]),
+    "gptrig_moe_router_logits": (I, [P, P, P, I, I, I, P]),
+    "gptrig_moe_gmm": (I, [P, P, L, P, I, P, P, I, P, P, L, I, I, I, I, P]),
+    "gptrig_moe_gmm_dw": (I, [P, P, L, P, L, P, P, P, I, I, I, I, P]),
+    "gptrig_moe_combine": (I, [P, P, P, P, I, I, I, P]),
+    "gptrig_moe_combine_bwd": (I, [P, P, P, P, P, P, I, I, I, P]),
+    "gptrig_moe_gather_bwd": (I, [P, P, P, I, I, I, P]),
+    "gptrig_moe_stats": (I, [P, P, P, P, I, I, I, P, P, P, P]),
+    "gptrig_moe_router_bwd": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
 }
 
 _LIB = None

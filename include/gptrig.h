@@ -171,13 +171,75 @@ int gptrig_fill_f32(float* x, int64_t n, float value, void* stream);
  *     chosen logits;
  *   counts i32 [experts] = assignments per expert;
  *   order i32 [tokens*top_k] = stable argsort of chosen.reshape(-1);
- *   rows i32 [tokens*top_k] = order / top_k (the source token of each slot).
+ *   rows i32 [tokens*top_k] = order / top_k (the source token of each slot);
+ *   position i32 [tokens*top_k] (nullable) = inverse of order: the bucket
+ *     row of assignment t*top_k + j.
  * workspace: gptrig_moe_route_workspace_bytes(tokens, experts, top_k).
  * ---------------------------------------------------------------------- */
 size_t gptrig_moe_route_workspace_bytes(int tokens, int experts, int top_k);
 int gptrig_moe_route(const float* logits, float* probs, int32_t* chosen, float* gate, int32_t* counts,
-                     int32_t* order, int32_t* rows, void* workspace, size_t workspace_bytes, int tokens, int experts,
-                     int top_k, void* stream);
+                     int32_t* order, int32_t* rows, int32_t* position, void* workspace, size_t workspace_bytes,
+                     int tokens, int experts, int top_k, void* stream);
+
+/* Router logits of routed_mlp_local (reference_moe/train.py:1259-1264):
+ * logits f32 [tokens, experts] = f32(x) @ router_w, x bf16 [tokens, width],
+ * router_w f32 [width, experts]; experts <= 16, width * experts <= 8192. */
+int gptrig_moe_router_logits(const void* x, const float* router_w, float* logits, int tokens, int width, int experts,
+                             void* stream);
+
+/* Grouped expert GEMM, the megablox.gmm calls of routed_mlp_local
+ * (reference_moe/train.py:1279-1285) with their bias / GELU epilogues:
+ * for each expert e and each of its counts[e] bucket rows r (buckets are
+ * consecutive in expert order, rows = sum(counts)):
+ *   acc[r][j] = sum_i lhs[row(r)][i] * W_e(i, j),
+ *   row(r) = lhs_rows ? lhs_rows[r] : r   (lhs bf16, leading dim lda),
+ *   W_e = rhs + e*k*n as bf16 [k][n], or as [n][k] (its transpose) when
+ *   rhs_transposed (the input-gradient GEMM of the backward);
+ *   mode 0: out = bf16(acc) (+ bias[e][j] when bias is not NULL)
+ *   mode 1: pre = bf16(bf16(acc) + bias[e][j]), out = bf16(gelu_tanh(pre))
+ *   mode 2: out = bf16(bf16(acc) * gelu_tanh'(pre))   (pre is an input)
+ * out / pre bf16 [rows, n] with leading dim ldo; k, n multiples of 8. */
+int gptrig_moe_gmm(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* rhs, int rhs_transposed,
+                   const int32_t* counts, const void* bias, int mode, void* out, void* pre, int64_t ldo, int rows,
+                   int k, int n, int experts, void* stream);
+
+/* Expert weight and bias gradients (the transposed gmm of the backward):
+ * dw f32 [experts, k, n] += sum over bucket rows r of expert e of
+ * lhs[row(r)][i] * dy[r][j]; db f32 [experts, n] (nullable) += column sums of
+ * dy over each bucket.  fp32 atomics. */
+int gptrig_moe_gmm_dw(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* dy, int64_t ldy,
+                      const int32_t* counts, float* dw, float* db, int rows, int k, int n, int experts,
+                      void* stream);
+
+/* Gated combine (reference_moe/train.py:1287-1288): combined bf16 [tokens,
+ * width] = sum over the token's top_k bucket rows, in bucket order, of
+ * bf16(out[p] * bf16(gate)), accumulated in bf16 like zeros.at[rows].add.
+ * position from gptrig_moe_route; top_k <= 8. */
+int gptrig_moe_combine(const void* out, const int32_t* position, const float* gate, void* combined, int tokens,
+                       int width, int top_k, void* stream);
+/* Its VJP: dout bf16 [rows, width] = dcombined[t] * bf16(gate[a]) at the
+ * slot's bucket row, dgate f32 [tokens*top_k] = <dcombined[t], out[p]>. */
+int gptrig_moe_combine_bwd(const void* dcombined, const void* out, const int32_t* position, const float* gate,
+                           void* dout, float* dgate, int tokens, int width, int top_k, void* stream);
+/* VJP of grouped = flat[rows]: dx bf16 [tokens, width] = bf16 sum over the
+ * token's bucket rows (bucket order) of dgrouped. */
+int gptrig_moe_gather_bwd(const void* dgrouped, const int32_t* position, void* dx, int tokens, int width, int top_k,
+                          void* stream);
+
+/* Router statistics of routed_mlp_local (reference_moe/train.py:1290-1306):
+ * mean_probability f32 [experts], load f32 [experts] = counts / (tokens *
+ * top_k), summary f32 [3] = (mean entropy, mean top-1 gate, logit RMS). */
+int gptrig_moe_stats(const float* logits, const float* probs, const float* gate, const int32_t* counts, int tokens,
+                     int experts, int top_k, float* mean_probability, float* load, float* summary, void* stream);
+
+/* Router backward: gate-softmax and probability-softmax VJPs (dgate from
+ * gptrig_moe_combine_bwd; dmean_probability f32 [experts] nullable, the
+ * gradient of the balance loss w.r.t. mean_probability, load_balance_loss
+ * :1347-1371), then dx bf16 [tokens, width] += bf16(dlogits @ router_w^T)
+ * in place and dw_router f32 [width, experts] += f32(x)^T dlogits. */
+int gptrig_moe_router_bwd(const void* x, const float* router_w, const float* probs, const int32_t* chosen,
+                          const float* gate, const float* dgate, const float* dmean_probability, void* dx,
+                          float* dw_router, int tokens, int width, int experts, int top_k, void* stream);
 
 #ifdef __cplusplus
 }

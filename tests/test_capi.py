@@ -52,7 +52,7 @@ def test_host_validation_rejects_bad_arguments_without_launching():
     assert lib.gptrig_adamw(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 1000, 0.1, 0.9, 0.95, 1, None, None,
                             None) == -2
     # routing: too many experts
-    assert lib.gptrig_moe_route(dummy, None, dummy, dummy, dummy, dummy, dummy, None, 0, 8, 65, 2, None) == -4
+    assert lib.gptrig_moe_route(dummy, None, dummy, dummy, dummy, dummy, dummy, None, None, 0, 8, 65, 2, None) == -4
 
 
 def test_workspace_queries_are_bounded_by_the_chunk():

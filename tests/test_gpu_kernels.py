@@ -331,13 +331,19 @@ def test_moe_routing_bit_exact():
     counts = torch.empty(E, dtype=torch.int32, device=DEV)
     order = torch.empty(T * k, dtype=torch.int32, device=DEV)
     rows = torch.empty(T * k, dtype=torch.int32, device=DEV)
+    position = torch.empty(T * k, dtype=torch.int32, device=DEV)
     _lib.call("gptrig_moe_route", lg.data_ptr(), probs.data_ptr(), chosen.data_ptr(), gate.data_ptr(),
-              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), None, 0, T, E, k, _lib.stream())
+              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), None, 0, T, E, k,
+              _lib.stream())
     torch.cuda.synchronize()
     assert torch.equal(chosen.cpu(), chosen_r)
     assert torch.equal(counts.cpu(), counts_r)
     assert torch.equal(order.cpu().long(), order_r)
     assert torch.equal(rows.cpu().long(), rows_r)
+    # position is the inverse permutation of order.
+    inv = torch.empty_like(order_r)
+    inv[order_r] = torch.arange(T * k)
+    assert torch.equal(position.cpu().long(), inv)
     assert float((gate.cpu() - gate_r).abs().max()) <= 1e-6
     assert float((probs.cpu() - probs_r).abs().max()) <= 1e-6
 
