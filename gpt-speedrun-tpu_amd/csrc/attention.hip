@@ -669,8 +669,11 @@ __global__ void __launch_bounds__(256, 2)
 // transposed reads, so nothing is written to LDS transposed.  dS is stored as
 // dS^T [key][query] (8-byte writes) and dQ = dS K is added to an fp32
 // accumulator with atomics.
+#ifndef GPTRIG_BWD64_OCC
+#define GPTRIG_BWD64_OCC 2
+#endif
 template <bool kSeg>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
     attn_bwd64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
                       const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
                       MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2) {

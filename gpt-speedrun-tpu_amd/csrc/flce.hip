@@ -31,12 +31,11 @@ using gemm::Operand;
 __global__ void __launch_bounds__(gemm::THREADS)
     flce_fwd_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, const int32_t* __restrict__ targets,
                     float2* __restrict__ partial, float* __restrict__ tlogit) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
   __shared__ float2 xchg[4][64];
   int tm, tn;
   gemm::tile_coords(blockIdx.x, V, N, tm, tn);
   f32x16 acc[4][2];
-  gemm::mainloop<true, true>(acc, W, Hd, V, N, 0, D, tm * BM, tn * BN, lds);
+  gemm::mainloop<true, true>(acc, W, Hd, V, N, 0, D, tm * BM, tn * BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
@@ -108,11 +107,10 @@ __global__ void __launch_bounds__(gemm::THREADS)
     flce_grad_kernel(Operand W, Operand Hd, int Vc, int N, int D, int v0, int sem_v,
                      const int32_t* __restrict__ targets, const float* __restrict__ lse,
                      const float* __restrict__ cot, float cot_scale, bf16* __restrict__ gt) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
   int tm, tn;
   gemm::tile_coords(blockIdx.x, Vc, N, tm, tn);
   f32x16 acc[4][2];
-  gemm::mainloop<true, true>(acc, W, Hd, Vc, N, 0, D, tm * BM, tn * BN, lds);
+  gemm::mainloop<true, true>(acc, W, Hd, Vc, N, 0, D, tm * BM, tn * BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
@@ -151,7 +149,7 @@ template <bool AK, bool BKM>
 __global__ void __launch_bounds__(gemm::THREADS)
     gemm_f32_kernel(Operand A, Operand B, int M, int N, int K, int ksplit, float* __restrict__ C, int64_t ldc,
                     int mode, float* __restrict__ colsum) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
+  __shared__ float red[8 * 256];
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int split = blockIdx.x / tiles;
   int tm, tn;
@@ -163,12 +161,10 @@ __global__ void __launch_bounds__(gemm::THREADS)
   f32x16 acc[4][2];
   f32x4 csum = f32x4{};
   const bool do_colsum = !BKM && colsum != nullptr && tm == 0;
-  gemm::mainloop<AK, BKM, !BKM>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, lds, &csum, do_colsum);
+  gemm::mainloop<AK, BKM, !BKM>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, &csum, do_colsum);
   if (k_begin >= k_end) return;
   if (do_colsum) {
-    // Reduce the 8 row groups of each column through LDS (the mainloop ended
-    // with a barrier, so the slabs are free).
-    float* red = reinterpret_cast<float*>(lds);
+    // Reduce the 8 row groups of each column through LDS.
     const int n4 = (tid & 63) * 4, grp = tid >> 6;
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[grp * 256 + n4 + j] = csum[j];

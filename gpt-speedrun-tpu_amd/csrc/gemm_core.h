@@ -1,47 +1,70 @@
 // bf16 MFMA GEMM core for gfx950: C[m][n] = sum_k A(m,k) B(k,n), fp32 accumulate.
 //
-// Workgroup tile 256 x 256 x 64, 512 threads = 8 waves laid out 2 (M) x 4 (N),
-// each wave owning a 128 x 64 sub-tile as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16.
-// LDS is double buffered (2 operands x 2 stages, 144 KB).
+// Workgroup tile 256 x 256, 512 threads = 8 waves laid out 2 (M) x 4 (N),
+// each wave owning a 128 x 64 sub-tile as 4 x 2 blocks of
+// v_mfma_f32_32x32x16_bf16.  K advances in stages of 32.
+//
+// Operand staging: global_load_lds_dwordx4 copies each 16-byte chunk straight
+// from global memory into LDS (no registers, no LDS store instructions),
+// through a 4-stage ring of separate LDS arrays (4 x 32 KB).  Stage kt is
+// waited for with an exact vmcnt (the loads of the two younger stages stay in
+// flight) followed by a bare s_barrier -- __syncthreads() would drain every
+// outstanding load.  Keeping the stages in separate arrays lets the compiler
+// see that LDS reads of one stage never alias the copies into another, so it
+// inserts no vmcnt(0) before them.
 //
 // Each operand is K-major (A[m*ld + k], B[n*ld + k]) or MN-major
-// (A[k*ld + m], B[k*ld + n]).  Both are copied to LDS in their natural layout
-// with 16-byte stores.  K-major fragments are one 16-byte LDS read per lane;
-// MN-major fragments use ds_read_b64_tr_b16, which hands each lane of a
-// 16-lane group the column of a 4 x 16 block: lane c supplies the address of
-// row k0 + c/4, columns m0 + 4(c%4) .. +3, and lane i receives rows k0..k0+3 of
-// column m0 + i.  Two such reads give the 8 k-values of one MFMA operand.
+// (A[k*ld + m], B[k*ld + n]) and is copied in its natural layout:
+//   K-major slab:  256 rows x 32 k = 64 B rows of 4 chunks; chunk c of row r
+//                  sits at position c ^ ((r >> 2) & 3), so the 16 rows a
+//                  quarter-wave reads at one chunk hit 16 distinct 16-byte
+//                  bank groups;
+//   MN-major slab: 32 k-rows x 256 = 512 B rows of 32 chunks; chunk c of row
+//                  k sits at position c ^ (4 (k & 3)), so the 4 rows x 4
+//                  chunks a half-wave of ds_read_b64_tr_b16 touches hit
+//                  distinct bank groups.
+// The swizzle is applied on the global side: lane L of a load writes LDS bytes
+// [16L, 16L+16) of its 1 KB block and fetches whichever chunk belongs there.
+// K-major fragments are one 16-byte LDS read per lane; MN-major fragments use
+// ds_read_b64_tr_b16, which hands lane i of a 16-lane group the column of a
+// 4 x 16 block: lane c supplies the address of row k0 + c/4, columns
+// m0 + 4(c%4) .. +3, and lane i receives rows k0..k0+3 of column m0 + i.
+//
+// Per-lane global addresses are computed once per tile; a stage only adds a
+// stride.  Fragment reads of the next half-stage are issued before the MFMAs
+// of the current one, so LDS latency hides behind the matrix core.
 #pragma once
 
 #include "common.h"
 
 namespace gemm {
 
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 256, BN = 256, BK = 32;
 constexpr int THREADS = 512;
-constexpr int KLD = BK + 8;         // K-major LDS row stride (elements), 144 B rows
-constexpr int MLD = 256 + 32;       // MN-major LDS row stride: 576 B rows, 144 dwords == 16 (mod 64 banks)
-constexpr int SLAB = 256 * KLD;     // elements per operand per stage (>= BK * MLD)
-static_assert(BK * MLD <= SLAB, "MN-major slab must fit");
-constexpr int LDS_BYTES = 4 * SLAB * 2;
+constexpr int OPE = 256 * BK;  // elements per operand slab of one stage (16 KB)
+constexpr int STE = 2 * OPE;   // A slab then B slab
 constexpr int kGroupM = 8;
+
+__shared__ __attribute__((aligned(1024))) bf16 g_stage0[STE];
+__shared__ __attribute__((aligned(1024))) bf16 g_stage1[STE];
+__shared__ __attribute__((aligned(1024))) bf16 g_stage2[STE];
+__shared__ __attribute__((aligned(1024))) bf16 g_stage3[STE];
+__device__ const bf16x8 g_zero_chunk[4] = {};
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 // Address-space-qualified views: LDS (3) so fragment traffic is ds_read/ds_write,
 // global (1) so operand loads are global_load rather than flat.
 typedef __attribute__((address_space(3))) bf16 lds_t;
 typedef __attribute__((address_space(3))) bf16x8 lds_x8;
+typedef __attribute__((address_space(3))) bf16x4 lds_x4;
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
 typedef const __attribute__((address_space(1))) bf16x8 gbl_x8;
 
-// Element (row r, column c) of the stored matrix is p[row(r) * ld + c] with
-// row(r) = idx ? idx[r] : r: idx gathers rows (K-major: M/N rows; MN-major:
-// k rows), which is how the routed expert GEMMs read token rows in bucket
-// order without a gathered copy.
 struct Operand {
   const bf16* p;
   int64_t ld;
-  const int32_t* idx = nullptr;
 };
 
 __device__ __forceinline__ lds_t* lds_cast(bf16* p) { return (lds_t*)p; }
@@ -51,63 +74,175 @@ __device__ __forceinline__ bf16x4 read_tr(const lds_t* lds) {
   return __builtin_bit_cast(bf16x4, r);
 }
 
-// Global -> registers: 4 x 16 bytes per thread per 256 x 64 slab.
+template <int S>
+__device__ __forceinline__ lds_t* stage_ptr() {
+  if constexpr (S == 0) return (lds_t*)g_stage0;
+  else if constexpr (S == 1) return (lds_t*)g_stage1;
+  else if constexpr (S == 2) return (lds_t*)g_stage2;
+  else return (lds_t*)g_stage3;
+}
+
+// Per-lane copy sources of one operand: the wave fills 1 KB blocks 2w and
+// 2w+1 of each 16 KB slab.  base[j] is the global address at stage 0, step
+// the per-stage stride, nvalid[j] the number of stages whose 16 bytes lie in
+// [k_begin, k_end) and inside the M/N extent (later stages read zeros).
+struct Src {
+  const bf16* base[2];
+  int64_t step;
+  int nvalid[2];
+};
+
 template <bool KMAJOR>
-__device__ __forceinline__ void load_slab(bf16x8 (&st)[4], Operand op, int mn0, int k0, int MN, int K, int tid) {
+__device__ __forceinline__ Src make_src(Operand op, int mn0, int k_begin, int MN, int k_end, int wave, int lane) {
+  Src s;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int idx = tid + THREADS * r;
+  for (int j = 0; j < 2; ++j) {
+    const int blk = 2 * wave + j;
     if (KMAJOR) {
-      const int row = idx >> 3, kc = (idx & 7) * 8;
-      const int m = mn0 + row, k = k0 + kc;
-      if (m < MN && k < K) {
-        const int64_t pr = op.idx ? op.idx[m] : m;
-        st[r] = *(gbl_x8*)(op.p + pr * op.ld + k);
-      } else {
-        st[r] = bf16x8{};
-      }
+      const int row = blk * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ ((row >> 2) & 3);
+      const int m = mn0 + row;
+      s.base[j] = op.p + (int64_t)(m < MN ? m : 0) * op.ld + k_begin + 8 * c;
+      const int rem = k_end - k_begin - 8 * c;
+      s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
     } else {
-      const int kk = idx >> 5, mc = (idx & 31) * 8;
-      const int m = mn0 + mc, k = k0 + kk;
-      if (m < MN && k < K) {
-        const int64_t pk = op.idx ? op.idx[k] : k;
-        st[r] = *(gbl_x8*)(op.p + pk * op.ld + m);
-      } else {
-        st[r] = bf16x8{};
-      }
+      const int row = blk * 2 + (lane >> 5);
+      const int c = (lane & 31) ^ (4 * (row & 3));
+      const int m = mn0 + 8 * c;
+      s.base[j] = op.p + (int64_t)(k_begin + row) * op.ld + (m < MN ? m : 0);
+      const int rem = k_end - k_begin - row;
+      s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
     }
+  }
+  s.step = KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld;
+  return s;
+}
+
+__device__ __forceinline__ void issue(lds_t* slab, const Src& s, int kt, int wave) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int blk = 2 * wave + j;
+    const bf16* src = kt < s.nvalid[j] ? s.base[j] + kt * s.step : (const bf16*)g_zero_chunk;
+    __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(slab + blk * 512), 16, 0, 0);
   }
 }
 
+// MFMA operand (8 k-values) for rows r0 .. r0+31 at k-chunk kc (0 or 1) of a slab.
 template <bool KMAJOR>
-__device__ __forceinline__ void store_slab(lds_t* lds, const bf16x8 (&st)[4], int tid) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int idx = tid + THREADS * r;
-    if (KMAJOR) {
-      const int row = idx >> 3, kc = (idx & 7) * 8;
-      *(lds_x8*)(lds + row * KLD + kc) = st[r];
-    } else {
-      const int kk = idx >> 5, mc = (idx & 31) * 8;
-      *(lds_x8*)(lds + kk * MLD + mc) = st[r];
-    }
-  }
-}
-
-// MFMA operand (8 k-values) for rows r0 .. r0+31 at k-chunk kc of a slab.
-template <bool KMAJOR>
-__device__ __forceinline__ bf16x8 frag(const lds_t* lds, int r0, int kc, int lane) {
+__device__ __forceinline__ bf16x8 frag(const lds_t* slab, int r0, int kc, int lane) {
   const int hl = lane >> 5;
   if (KMAJOR) {
-    return *(const lds_x8*)(lds + (r0 + (lane & 31)) * KLD + 16 * kc + 8 * hl);
+    const int row = r0 + (lane & 31);
+    const int c = 2 * kc + hl;
+    return *(const lds_x8*)(slab + row * BK + 8 * (c ^ ((row >> 2) & 3)));
   } else {
-    const int c = lane & 15;
-    const int m = r0 + 16 * ((lane >> 4) & 1) + 4 * (c & 3);
-    const int k = 16 * kc + 8 * hl + (c >> 2);
-    bf16x4 lo = read_tr(lds + k * MLD + m);
-    bf16x4 hi = read_tr(lds + (k + 4) * MLD + m);
+    const int cq = lane & 15;
+    const int m = r0 + 16 * ((lane >> 4) & 1) + 4 * (cq & 3);
+    const int k = 16 * kc + 8 * hl + (cq >> 2);
+    const int off = 8 * ((m >> 3) ^ (4 * (k & 3))) + 4 * ((m >> 2) & 1);
+    bf16x4 lo = read_tr(slab + k * 256 + off), hi = read_tr(slab + (k + 4) * 256 + off);
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
+}
+
+// Column sums of an MN-major B slab of one stage: thread t adds rows
+// 4(t/64) .. +3 of columns 4(t%64) .. +3 (one 8-byte read per row) into sum.
+__device__ __forceinline__ void colsum_slab(f32x4& sum, const lds_t* slab, int tid) {
+  const int n4 = (tid & 63) * 4, k0 = (tid >> 6) * 4;
+#pragma unroll
+  for (int k = k0; k < k0 + 4; ++k) {
+    const int off = 8 * ((n4 >> 3) ^ (4 * (k & 3))) + (n4 & 7);
+    const bf16x4 v = *(const lds_x4*)(slab + k * 256 + off);
+    sum[0] += (float)v[0];
+    sum[1] += (float)v[1];
+    sum[2] += (float)v[2];
+    sum[3] += (float)v[3];
+  }
+}
+
+// s_waitcnt immediates (gfx9 layout: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8]).
+#define GEMM_WAIT_VM8_LGKM0() __builtin_amdgcn_s_waitcnt(0x0078)
+#define GEMM_WAIT_VM12_LGKM0() __builtin_amdgcn_s_waitcnt(0x007C)
+#define GEMM_WAIT_VM0_LGKM0() __builtin_amdgcn_s_waitcnt(0x0070)
+
+struct Ctx {
+  Src sa, sb;
+  int wm0, wn0, wave, lane, tid;
+};
+
+template <bool AK, bool BKM>
+__device__ __forceinline__ void read_half(bf16x8 (&a)[4], bf16x8 (&b)[2], const lds_t* st, int kc, const Ctx& c) {
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) a[mb] = frag<AK>(st, c.wm0 + 32 * mb, kc, c.lane);
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) b[nb] = frag<BKM>(st + OPE, c.wn0 + 32 * nb, kc, c.lane);
+}
+
+__device__ __forceinline__ void mma_half(f32x16 (&acc)[4][2], const bf16x8 (&a)[4], const bf16x8 (&b)[2]) {
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(a[mb], b[nb], acc[mb][nb]);
+}
+
+__device__ __forceinline__ void fill(lds_t* st, const Ctx& c, int kt) {
+  issue(st, c.sa, kt, c.wave);
+  issue(st + OPE, c.sb, kt, c.wave);
+}
+
+// One stage: on entry a0/b0 hold k-chunk 0 of stage kt (buffer S).  Reads
+// chunk 1, runs chunk 0's MFMAs, waits for stage kt+1 and the barrier (every
+// wave is done with buffer S), refills S with stage kt+4, reads chunk 0 of
+// stage kt+1, runs chunk 1's MFMAs.
+template <bool AK, bool BKM, bool kColSum, int S>
+__device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, bf16x8 (&a0)[4], bf16x8 (&b0)[2],
+                                     f32x4* colsum, bool colsum_on) {
+  bf16x8 a1[4], b1[2];
+  read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
+  if (kColSum && colsum_on) colsum_slab(*colsum, stage_ptr<S>() + OPE, c.tid);
+  mma_half(acc, a0, b0);
+  GEMM_WAIT_VM8_LGKM0();
+  __builtin_amdgcn_s_barrier();
+  fill(stage_ptr<S>(), c, kt + 4);
+  read_half<AK, BKM>(a0, b0, stage_ptr<(S + 1) % 4>(), 0, c);
+  mma_half(acc, a1, b1);
+}
+
+// acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
+// with wm0 = 128*(wave&1), wn0 = 64*(wave>>1); K range [k_begin, k_end).
+// With kColSum (MN-major B only) and colsum_on, colsum also accumulates the
+// column sums of B over the K range (see colsum_slab for the thread mapping).
+// Uses the four stage arrays; on return no copy into them is in flight, but
+// other waves may still read the last stage: barrier before reusing them.
+template <bool AK, bool BKM, bool kColSum = false>
+__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
+                                         int k_end, int tm0, int tn0, f32x4* colsum = nullptr,
+                                         bool colsum_on = false) {
+  static_assert(!kColSum || !BKM, "column sums need an MN-major B operand");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
+  const int nk = (k_end - k_begin + BK - 1) / BK;
+  if (nk <= 0) return;
+  const Ctx c{make_src<AK>(A, tm0, k_begin, M, k_end, wave, lane), make_src<BKM>(B, tn0, k_begin, N, k_end, wave, lane),
+              128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid};
+  fill(stage_ptr<0>(), c, 0);
+  fill(stage_ptr<1>(), c, 1);
+  fill(stage_ptr<2>(), c, 2);
+  fill(stage_ptr<3>(), c, 3);
+  GEMM_WAIT_VM12_LGKM0();
+  __builtin_amdgcn_s_barrier();
+  bf16x8 a0[4], b0[2];
+  read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
+  for (int kt = 0; kt < nk; kt += 4) {
+    step<AK, BKM, kColSum, 0>(acc, c, kt, a0, b0, colsum, colsum_on);
+    if (kt + 1 < nk) step<AK, BKM, kColSum, 1>(acc, c, kt + 1, a0, b0, colsum, colsum_on);
+    if (kt + 2 < nk) step<AK, BKM, kColSum, 2>(acc, c, kt + 2, a0, b0, colsum, colsum_on);
+    if (kt + 3 < nk) step<AK, BKM, kColSum, 3>(acc, c, kt + 3, a0, b0, colsum, colsum_on);
+  }
+  GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
@@ -128,73 +263,6 @@ __device__ __forceinline__ void tile_coords(int pid, int M, int N, int& tm, int&
   const int gsize = min(mt - first_m, kGroupM);
   tm = first_m + (pid % in_group) % gsize;
   tn = (pid % in_group) / gsize;
-}
-
-// Column sums of an MN-major B slab: thread t adds rows 8(t/64) .. +7 of
-// columns 4(t%64) .. +3 (one 8-byte LDS read per row) into sum.
-__device__ __forceinline__ void colsum_slab(f32x4& sum, const lds_t* lb, int tid) {
-  const int n4 = (tid & 63) * 4, k0 = (tid >> 6) * 8;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const bf16x4 v = *(const __attribute__((address_space(3))) bf16x4*)(lb + (k0 + k) * MLD + n4);
-    sum[0] += (float)v[0];
-    sum[1] += (float)v[1];
-    sum[2] += (float)v[2];
-    sum[3] += (float)v[3];
-  }
-}
-
-// acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
-// with wm0 = 128*(wave&1), wn0 = 64*(wave>>1); K range [k_begin, k_end).
-// With kColSum (MN-major B only) and colsum_on, colsum also accumulates the
-// column sums of B over the K range (see colsum_slab for the thread mapping).
-template <bool AK, bool BKM, bool kColSum = false>
-__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
-                                         int k_end, int tm0, int tn0, bf16* lds, f32x4* colsum = nullptr,
-                                         bool colsum_on = false) {
-  static_assert(!kColSum || !BKM, "column sums need an MN-major B operand");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm0 = 128 * (wave & 1), wn0 = 64 * (wave >> 1);
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
-  const int nk = (k_end - k_begin + BK - 1) / BK;
-  if (nk <= 0) return;
-  lds_t* const lbase = lds_cast(lds);
-  bf16x8 sa[4], sb[4];
-  load_slab<AK>(sa, A, tm0, k_begin, M, k_end, tid);
-  load_slab<BKM>(sb, B, tn0, k_begin, N, k_end, tid);
-  store_slab<AK>(lbase, sa, tid);
-  store_slab<BKM>(lbase + 2 * SLAB, sb, tid);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const lds_t* la = lbase + buf * SLAB;
-    const lds_t* lb = lbase + (2 + buf) * SLAB;
-    if (kt + 1 < nk) {
-      load_slab<AK>(sa, A, tm0, k_begin + (kt + 1) * BK, M, k_end, tid);
-      load_slab<BKM>(sb, B, tn0, k_begin + (kt + 1) * BK, N, k_end, tid);
-    }
-#pragma unroll
-    for (int kc = 0; kc < BK / 16; ++kc) {
-      bf16x8 fa[4], fb[2];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) fa[mb] = frag<AK>(la, wm0 + 32 * mb, kc, lane);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) fb[nb] = frag<BKM>(lb, wn0 + 32 * nb, kc, lane);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(fa[mb], fb[nb], acc[mb][nb]);
-    }
-    if (kColSum && colsum_on) colsum_slab(*colsum, lb, tid);
-    if (kt + 1 < nk) {
-      store_slab<AK>(lbase + (buf ^ 1) * SLAB, sa, tid);
-      store_slab<BKM>(lbase + (2 + (buf ^ 1)) * SLAB, sb, tid);
-    }
-    __syncthreads();
-  }
 }
 
 // ---- host side: launch shaping ----
@@ -219,7 +287,7 @@ inline int device_cus() {
 // grid a quarter full, which a fixed split does for skinny outputs.
 inline int choose_split(unsigned tiles, int k_iters) {
   const int cus = device_cus();
-  const int max_split = k_iters / 4 > 1 ? k_iters / 4 : 1;
+  const int max_split = k_iters / 8 > 1 ? k_iters / 8 : 1;
   double best = 1e30;
   int best_split = 1;
   for (int s = 1; s <= max_split && s <= 256; ++s) {

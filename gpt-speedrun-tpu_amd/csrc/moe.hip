@@ -10,9 +10,9 @@
 //
 // The routed MLP around it (:1275-1293):
 //   router_logits   fp32 x @ router_w (one wave per token, weights in LDS);
-//   moe_gmm         grouped GEMM over the expert buckets on the MFMA GEMM core:
-//                   A rows gathered through `rows` (no gathered copy), epilogue
-//                   bias (+ GELU, or x GELU' for the backward);
+//   moe_gather_rows grouped = flat[rows] (token rows in bucket order);
+//   moe_gmm         grouped GEMM over the expert buckets on the MFMA GEMM core,
+//                   epilogue bias (+ GELU, or x GELU' for the backward);
 //   moe_combine     combined[t] = sum over the token's slots, in bucket order,
 //                   of bf16(out * bf16(gate)) -- the .at[rows].add rounding;
 //   moe_stats       mean probability, load, (entropy, top-1 gate, logit RMS);
@@ -161,7 +161,7 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const bf16* __restri
 // ---------------------------------------------------------------------------
 // Grouped GEMM over the expert buckets (megablox.gmm contract):
 //   out[off_e + r][n] = sum_k A[off_e + r][k] * B_e(k, n),  r < counts[e],
-// A K-major [R][K] (row i read from a_idx ? a_idx[i] : i), B_e either [K][N]
+// A K-major [R][K] (rows in bucket order), B_e either [K][N]
 // (kBT = false: rhs + e*K*N) or [N][K] (kBT = true: the transpose, for dX).
 // Grid: (ceil(R/256) + E) M-tile slots x ceil(N/256); surplus slots exit.
 // kMode 0: out = bf16(acc) (+ bias)
@@ -170,10 +170,9 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const bf16* __restri
 // ---------------------------------------------------------------------------
 template <bool kBT, int kMode>
 __global__ void __launch_bounds__(gemm::THREADS)
-    moe_gmm_kernel(const bf16* __restrict__ lhs, const int32_t* __restrict__ a_idx, int64_t lda,
+    moe_gmm_kernel(const bf16* __restrict__ lhs, int64_t lda,
                    const bf16* __restrict__ rhs, const int32_t* __restrict__ counts, int E, int K, int N,
                    const bf16* __restrict__ bias, bf16* __restrict__ out, bf16* __restrict__ pre, int64_t ldo) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
   const int ntn = (N + gemm::BN - 1) / gemm::BN;
   const int tn = blockIdx.x % ntn;
   int tm = blockIdx.x / ntn;
@@ -187,10 +186,10 @@ __global__ void __launch_bounds__(gemm::THREADS)
   }
   if (e >= E) return;  // uniform: surplus slot
   const int cnt = counts[e];
-  gemm::Operand A{a_idx ? lhs : lhs + (int64_t)off * lda, lda, a_idx ? a_idx + off : nullptr};
+  gemm::Operand A{lhs + (int64_t)off * lda, lda};
   gemm::Operand B = kBT ? gemm::Operand{rhs + (int64_t)e * N * K, K} : gemm::Operand{rhs + (int64_t)e * K * N, N};
   f32x16 acc[4][2];
-  gemm::mainloop<true, kBT>(acc, A, B, cnt, N, 0, K, tm * gemm::BM, tn * gemm::BN, lds);
+  gemm::mainloop<true, kBT>(acc, A, B, cnt, N, 0, K, tm * gemm::BM, tn * gemm::BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
@@ -223,13 +222,13 @@ __global__ void __launch_bounds__(gemm::THREADS)
 // Per-expert weight (+ bias) gradients:
 //   dw[e] (f32 [K][N]) += sum_{r in bucket e} A[r][k] * dy[r][n],
 //   db[e] (f32 [N])    += sum_{r in bucket e} dy[r][n]          (nullable),
-// A [R][K] rows read through a_idx (nullable), dy [R][N].  Grid:
+// A [R][K] and dy [R][N] in bucket order.  Grid:
 // E x tiles(K, N) x split; bucket e's rows are split into `split` slices.
 __global__ void __launch_bounds__(gemm::THREADS)
-    moe_gmm_dw_kernel(const bf16* __restrict__ lhs, const int32_t* __restrict__ a_idx, int64_t lda,
+    moe_gmm_dw_kernel(const bf16* __restrict__ lhs, int64_t lda,
                       const bf16* __restrict__ dy, int64_t ldy, const int32_t* __restrict__ counts, int E, int K,
                       int N, int split, float* __restrict__ dw, float* __restrict__ db) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[4 * gemm::SLAB];
+  __shared__ float red[8 * 256];
   const int tiles = ((K + gemm::BM - 1) / gemm::BM) * ((N + gemm::BN - 1) / gemm::BN);
   const int e = blockIdx.x / (tiles * split);
   const int rem = blockIdx.x % (tiles * split);
@@ -244,13 +243,13 @@ __global__ void __launch_bounds__(gemm::THREADS)
   const int k_end = min(cnt, k_begin + kslice);
   if (k_begin >= k_end) return;  // uniform
   // A(m = k-index, k = bucket row) MN-major; B(k = bucket row, n) MN-major.
-  gemm::Operand A{a_idx ? lhs : lhs + (int64_t)off * lda, lda, a_idx ? a_idx + off : nullptr};
+  gemm::Operand A{lhs + (int64_t)off * lda, lda};
   gemm::Operand B{dy + (int64_t)off * ldy, ldy};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   f32x16 acc[4][2];
   f32x4 csum = f32x4{};
   const bool do_colsum = db != nullptr && tm == 0;
-  gemm::mainloop<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, lds, &csum,
+  gemm::mainloop<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, &csum,
                                      do_colsum);
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
@@ -268,7 +267,6 @@ __global__ void __launch_bounds__(gemm::THREADS)
       }
   }
   if (do_colsum) {
-    float* red = reinterpret_cast<float*>(lds);
     const int n4 = (tid & 63) * 4, grp = tid >> 6;
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[grp * 256 + n4 + j] = csum[j];
@@ -281,6 +279,17 @@ __global__ void __launch_bounds__(gemm::THREADS)
       if (n < N) atomicAdd(db + (int64_t)e * N + n, t);
     }
   }
+}
+
+// grouped[p] = x[rows[p]] (flat[rows], :1278): one wave per bucket row.
+__global__ void __launch_bounds__(256) moe_gather_rows_kernel(const bf16* __restrict__ x, const int32_t* __restrict__ rows,
+                                                              bf16* __restrict__ grouped, int R, int D) {
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (p >= R) return;
+  const int lane = threadIdx.x & 63;
+  const bf16* src = x + (size_t)rows[p] * D;
+  bf16* dst = grouped + (size_t)p * D;
+  for (int c = lane * 8; c < D; c += 512) *reinterpret_cast<bf16x8*>(dst + c) = *reinterpret_cast<const bf16x8*>(src + c);
 }
 
 // Sort the (at most kMaxTopK) bucket positions of one token ascending.
@@ -533,9 +542,19 @@ int gptrig_moe_router_logits(const void* x, const float* router_w, float* logits
   return GPTRIG_OK;
 }
 
-int gptrig_moe_gmm(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* rhs, int rhs_transposed,
-                   const int32_t* counts, const void* bias, int mode, void* out, void* pre, int64_t ldo, int rows,
-                   int k, int n, int experts, void* stream) {
+int gptrig_moe_gather_rows(const void* x, const int32_t* rows, void* grouped, int n_rows, int width, void* stream) {
+  if (!x || !rows || !grouped) return GPTRIG_E_NULL;
+  if (n_rows <= 0 || width <= 0 || width % 8) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)x | (uintptr_t)grouped) & 15) return GPTRIG_E_SHAPE;
+  moe_gather_rows_kernel<<<ceil_div(n_rows, 4), 256, 0, (hipStream_t)stream>>>((const bf16*)x, rows, (bf16*)grouped,
+                                                                               n_rows, width);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_moe_gmm(const void* lhs, int64_t lda, const void* rhs, int rhs_transposed, const int32_t* counts,
+                   const void* bias, int mode, void* out, void* pre, int64_t ldo, int rows, int k, int n, int experts,
+                   void* stream) {
   if (!lhs || !rhs || !counts || !out) return GPTRIG_E_NULL;
   if ((mode == 1 || mode == 2) && !pre) return GPTRIG_E_NULL;
   if (rows <= 0 || k <= 0 || n <= 0 || experts <= 0 || mode < 0 || mode > 2) return GPTRIG_E_SHAPE;
@@ -550,8 +569,7 @@ int gptrig_moe_gmm(const void* lhs, const int32_t* lhs_rows, int64_t lda, const 
   bf16* O = (bf16*)out;
   bf16* P = (bf16*)pre;
 #define GPTRIG_GMM(BT, MODE)                                                                                     \
-  moe_gmm_kernel<BT, MODE><<<grid, gemm::THREADS, 0, s>>>(L, lhs_rows, lda, Rh, counts, experts, k, n, Bi, O, P, \
-                                                          ldo)
+  moe_gmm_kernel<BT, MODE><<<grid, gemm::THREADS, 0, s>>>(L, lda, Rh, counts, experts, k, n, Bi, O, P, ldo)
   if (rhs_transposed) {
     if (mode == 0) GPTRIG_GMM(true, 0);
     else if (mode == 1) GPTRIG_GMM(true, 1);
@@ -566,9 +584,8 @@ int gptrig_moe_gmm(const void* lhs, const int32_t* lhs_rows, int64_t lda, const 
   return GPTRIG_OK;
 }
 
-int gptrig_moe_gmm_dw(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* dy, int64_t ldy,
-                      const int32_t* counts, float* dw, float* db, int rows, int k, int n, int experts,
-                      void* stream) {
+int gptrig_moe_gmm_dw(const void* lhs, int64_t lda, const void* dy, int64_t ldy, const int32_t* counts, float* dw,
+                      float* db, int rows, int k, int n, int experts, void* stream) {
   if (!lhs || !dy || !counts || !dw) return GPTRIG_E_NULL;
   if (rows <= 0 || k <= 0 || n <= 0 || experts <= 0) return GPTRIG_E_SHAPE;
   if (k % 8 || n % 8 || lda % 8 || ldy % 8 || lda < k || ldy < n) return GPTRIG_E_SHAPE;
@@ -577,7 +594,7 @@ int gptrig_moe_gmm_dw(const void* lhs, const int32_t* lhs_rows, int64_t lda, con
   const unsigned tiles = (unsigned)(ceil_div(k, gemm::BM) * ceil_div(n, gemm::BN));
   const int split = gemm::choose_split(tiles * experts, ceil_div(ceil_div(rows, experts), gemm::BK));
   moe_gmm_dw_kernel<<<tiles * experts * split, gemm::THREADS, 0, (hipStream_t)stream>>>(
-      (const bf16*)lhs, lhs_rows, lda, (const bf16*)dy, ldy, counts, experts, k, n, split, dw, db);
+      (const bf16*)lhs, lda, (const bf16*)dy, ldy, counts, experts, k, n, split, dw, db);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

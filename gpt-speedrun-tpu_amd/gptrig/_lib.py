@@ -53,8 +53,9 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_moe_route_workspace_bytes": (Z, [I, I, I]),
     "gptrig_moe_route": (I, [P, P, P, P, P, P, P, P, P, Z, I, I, I, P]),
     "gptrig_moe_router_logits": (I, [P, P, P, I, I, I, P]),
-    "gptrig_moe_gmm": (I, [P, P, L, P, I, P, P, I, P, P, L, I, I, I, I, P]),
-    "gptrig_moe_gmm_dw": (I, [P, P, L, P, L, P, P, P, I, I, I, I, P]),
+    "gptrig_moe_gather_rows": (I, [P, P, P, I, I, P]),
+    "gptrig_moe_gmm": (I, [P, L, P, I, P, P, I, P, P, L, I, I, I, I, P]),
+    "gptrig_moe_gmm_dw": (I, [P, L, P, L, P, P, P, I, I, I, I, P]),
     "gptrig_moe_combine": (I, [P, P, P, P, I, I, I, P]),
     "gptrig_moe_combine_bwd": (I, [P, P, P, P, P, P, I, I, I, P]),
     "gptrig_moe_gather_bwd": (I, [P, P, P, I, I, I, P]),

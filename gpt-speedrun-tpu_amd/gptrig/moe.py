@@ -38,12 +38,12 @@ def _route(flat: torch.Tensor, router_w: torch.Tensor, experts: int, top_k: int)
     return logits, probs, chosen, gate, counts, rows, position
 
 
-def _gmm(lhs, lhs_rows, rhs, transposed: bool, counts, bias, mode: int, pre, rows: int, k: int, n: int,
+def _gmm(lhs, rhs, transposed: bool, counts, bias, mode: int, pre, rows: int, k: int, n: int,
          experts: int) -> torch.Tensor:
     out = torch.empty((rows, n), dtype=BF16, device=lhs.device)
-    _lib.call("gptrig_moe_gmm", lhs.data_ptr(), None if lhs_rows is None else lhs_rows.data_ptr(), lhs.stride(0),
-              rhs.data_ptr(), int(transposed), counts.data_ptr(), None if bias is None else bias.data_ptr(), mode,
-              out.data_ptr(), None if pre is None else pre.data_ptr(), n, rows, k, n, experts, _lib.stream())
+    _lib.call("gptrig_moe_gmm", lhs.data_ptr(), lhs.stride(0), rhs.data_ptr(), int(transposed), counts.data_ptr(),
+              None if bias is None else bias.data_ptr(), mode, out.data_ptr(), None if pre is None else pre.data_ptr(),
+              n, rows, k, n, experts, _lib.stream())
     return out
 
 
@@ -59,9 +59,12 @@ class _RoutedMLP(torch.autograd.Function):
         logits, probs, chosen, gate, counts, rows, position = _route(flat, rw, experts, top_k)
         upw, upb = up_w.to(BF16).contiguous(), up_b.to(BF16).contiguous()
         dnw, dnb = down_w.to(BF16).contiguous(), down_b.to(BF16).contiguous()
+        grouped = torch.empty((R, width), dtype=BF16, device=x.device)
+        _lib.call("gptrig_moe_gather_rows", flat.data_ptr(), rows.data_ptr(), grouped.data_ptr(), R, width,
+                  _lib.stream())
         pre = torch.empty((R, hidden_width), dtype=BF16, device=x.device)
-        hidden = _gmm(flat, rows, upw, False, counts, upb, 1, pre, R, width, hidden_width, experts)
-        out = _gmm(hidden, None, dnw, False, counts, dnb, 0, None, R, hidden_width, width, experts)
+        hidden = _gmm(grouped, upw, False, counts, upb, 1, pre, R, width, hidden_width, experts)
+        out = _gmm(hidden, dnw, False, counts, dnb, 0, None, R, hidden_width, width, experts)
         combined = torch.empty((tokens, width), dtype=BF16, device=x.device)
         s = _lib.stream()
         _lib.call("gptrig_moe_combine", out.data_ptr(), position.data_ptr(), gate.data_ptr(), combined.data_ptr(),
@@ -71,7 +74,7 @@ class _RoutedMLP(torch.autograd.Function):
         summary = torch.empty(3, dtype=F32, device=x.device)
         _lib.call("gptrig_moe_stats", logits.data_ptr(), probs.data_ptr(), gate.data_ptr(), counts.data_ptr(), tokens,
                   experts, top_k, mean_probability.data_ptr(), load.data_ptr(), summary.data_ptr(), s)
-        ctx.save_for_backward(flat, rw, upw, dnw, probs, chosen, gate, counts, rows, position, pre, hidden, out)
+        ctx.save_for_backward(flat, grouped, rw, upw, dnw, probs, chosen, gate, counts, position, pre, hidden, out)
         ctx.meta = (batch, length, width, hidden_width, experts, top_k, x.dtype, router_w.dtype, up_w.dtype,
                     up_b.dtype, down_w.dtype, down_b.dtype)
         ctx.mark_non_differentiable(load, summary)
@@ -79,7 +82,7 @@ class _RoutedMLP(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dcombined, dmean_probability, _dload, _dsummary):
-        flat, rw, upw, dnw, probs, chosen, gate, counts, rows, position, pre, hidden, out = ctx.saved_tensors
+        flat, grouped, rw, upw, dnw, probs, chosen, gate, counts, position, pre, hidden, out = ctx.saved_tensors
         batch, length, width, hidden_width, experts, top_k, xdt, rdt, uwdt, ubdt, dwdt, dbdt = ctx.meta
         tokens = batch * length
         R = tokens * top_k
@@ -98,13 +101,13 @@ class _RoutedMLP(torch.autograd.Function):
         d_down_b = torch.zeros((experts, width), dtype=F32, device=dev)
         d_router = torch.zeros((width, experts), dtype=F32, device=dev)
         # Down projection: dW, db from (hidden, dout); d(pre) = (dout W^T) * gelu'(pre).
-        _lib.call("gptrig_moe_gmm_dw", hidden.data_ptr(), None, hidden_width, dout.data_ptr(), width,
-                  counts.data_ptr(), d_down_w.data_ptr(), d_down_b.data_ptr(), R, hidden_width, width, experts, s)
-        dpre = _gmm(dout, None, dnw, True, counts, None, 2, pre, R, width, hidden_width, experts)
-        # Up projection: dW, db from (gathered x rows, dpre); d(grouped) = dpre W^T.
-        _lib.call("gptrig_moe_gmm_dw", flat.data_ptr(), rows.data_ptr(), width, dpre.data_ptr(), hidden_width,
-                  counts.data_ptr(), d_up_w.data_ptr(), d_up_b.data_ptr(), R, width, hidden_width, experts, s)
-        dgrouped = _gmm(dpre, None, upw, True, counts, None, 0, None, R, hidden_width, width, experts)
+        _lib.call("gptrig_moe_gmm_dw", hidden.data_ptr(), hidden_width, dout.data_ptr(), width, counts.data_ptr(),
+                  d_down_w.data_ptr(), d_down_b.data_ptr(), R, hidden_width, width, experts, s)
+        dpre = _gmm(dout, dnw, True, counts, None, 2, pre, R, width, hidden_width, experts)
+        # Up projection: dW, db from (grouped, dpre); d(grouped) = dpre W^T.
+        _lib.call("gptrig_moe_gmm_dw", grouped.data_ptr(), width, dpre.data_ptr(), hidden_width, counts.data_ptr(),
+                  d_up_w.data_ptr(), d_up_b.data_ptr(), R, width, hidden_width, experts, s)
+        dgrouped = _gmm(dpre, upw, True, counts, None, 0, None, R, hidden_width, width, experts)
         dx = torch.empty((tokens, width), dtype=BF16, device=dev)
         _lib.call("gptrig_moe_gather_bwd", dgrouped.data_ptr(), position.data_ptr(), dx.data_ptr(), tokens, width,
                   top_k, s)

@@ -187,29 +187,32 @@ int gptrig_moe_route(const float* logits, float* probs, int32_t* chosen, float* 
 int gptrig_moe_router_logits(const void* x, const float* router_w, float* logits, int tokens, int width, int experts,
                              void* stream);
 
+/* Bucket-order copy of the token rows, grouped = flat[rows]
+ * (reference_moe/train.py:1278): grouped bf16 [n_rows, width] with
+ * grouped[p] = x[rows[p]]; width a multiple of 8. */
+int gptrig_moe_gather_rows(const void* x, const int32_t* rows, void* grouped, int n_rows, int width, void* stream);
+
 /* Grouped expert GEMM, the megablox.gmm calls of routed_mlp_local
  * (reference_moe/train.py:1279-1285) with their bias / GELU epilogues:
  * for each expert e and each of its counts[e] bucket rows r (buckets are
  * consecutive in expert order, rows = sum(counts)):
- *   acc[r][j] = sum_i lhs[row(r)][i] * W_e(i, j),
- *   row(r) = lhs_rows ? lhs_rows[r] : r   (lhs bf16, leading dim lda),
+ *   acc[r][j] = sum_i lhs[r][i] * W_e(i, j)   (lhs bf16, leading dim lda),
  *   W_e = rhs + e*k*n as bf16 [k][n], or as [n][k] (its transpose) when
  *   rhs_transposed (the input-gradient GEMM of the backward);
  *   mode 0: out = bf16(acc) (+ bias[e][j] when bias is not NULL)
  *   mode 1: pre = bf16(bf16(acc) + bias[e][j]), out = bf16(gelu_tanh(pre))
  *   mode 2: out = bf16(bf16(acc) * gelu_tanh'(pre))   (pre is an input)
  * out / pre bf16 [rows, n] with leading dim ldo; k, n multiples of 8. */
-int gptrig_moe_gmm(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* rhs, int rhs_transposed,
-                   const int32_t* counts, const void* bias, int mode, void* out, void* pre, int64_t ldo, int rows,
-                   int k, int n, int experts, void* stream);
+int gptrig_moe_gmm(const void* lhs, int64_t lda, const void* rhs, int rhs_transposed, const int32_t* counts,
+                   const void* bias, int mode, void* out, void* pre, int64_t ldo, int rows, int k, int n, int experts,
+                   void* stream);
 
 /* Expert weight and bias gradients (the transposed gmm of the backward):
  * dw f32 [experts, k, n] += sum over bucket rows r of expert e of
- * lhs[row(r)][i] * dy[r][j]; db f32 [experts, n] (nullable) += column sums of
+ * lhs[r][i] * dy[r][j]; db f32 [experts, n] (nullable) += column sums of
  * dy over each bucket.  fp32 atomics. */
-int gptrig_moe_gmm_dw(const void* lhs, const int32_t* lhs_rows, int64_t lda, const void* dy, int64_t ldy,
-                      const int32_t* counts, float* dw, float* db, int rows, int k, int n, int experts,
-                      void* stream);
+int gptrig_moe_gmm_dw(const void* lhs, int64_t lda, const void* dy, int64_t ldy, const int32_t* counts, float* dw,
+                      float* db, int rows, int k, int n, int experts, void* stream);
 
 /* Gated combine (reference_moe/train.py:1287-1288): combined bf16 [tokens,
  * width] = sum over the token's top_k bucket rows, in bucket order, of
