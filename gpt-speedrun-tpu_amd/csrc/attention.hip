@@ -21,6 +21,8 @@
 // atomics.  A last pass rounds dQ to bf16.
 #include "attn64.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kBlockM = 128;  // forward: queries per workgroup
@@ -773,69 +775,76 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
     load_q(qb + 1 < nqb ? qq0 + kBwdM : qq0);
 
     const bool wave_active = kw0 <= qq0 + kBwdM - 1 && kw0 < S;
+    // One 32-query half of the block.  kMask: the causal / ragged / segment
+    // mask is evaluated per element (diagonal and edge blocks only); the
+    // interior blocks run a mask-free copy of the same code.
+    auto qs_body = [&](int qs, auto mask_tag) {
+      constexpr bool kMask = decltype(mask_tag)::value;
+      bf16x8 qf[KC], gf[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        qf[kc] = at64::rowfrag(Qs, 32 * qs + l32, 2 * kc + hl);
+        gf[kc] = at64::rowfrag(dOs, 32 * qs + l32, 2 * kc + hl);
+      }
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        sacc = mfma32(qf[kc], kreg[kc], sacc);
+        pacc = mfma32(gf[kc], vreg[kc], pacc);
+      }
+      // Transposed operands of dV^T += dO^T P and dK^T += Q^T dS, read while
+      // the softmax below runs on the VALU.
+      bf16x8 gt[DB][2], qt[DB][2];
+#pragma unroll
+      for (int dbk = 0; dbk < DB; ++dbk)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          gt[dbk][c] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
+          qt[dbk][c] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
+        }
+      bf16x8 pb[2], db8[2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qr = 32 * qs + 8 * r + 4 * hl;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse_s[qr]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&delta_s[qr]);
+        bf16x4 ds4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int i = 4 * r + t;
+          float p = fast_exp2(fmaf(sacc[i], scale_log2, -l4[t]));
+          if (kMask) {
+            const int q = qq0 + qr + t;
+            bool vis = my_k <= q && q < S && k_ok;
+            if (kSeg && vis) vis = seg_s[qr + t] == seg_k;
+            p = vis ? p : 0.f;
+          }
+          const float ds = p * fmaf(pacc[i], scale, -d4[t]);
+          pb[i >> 3][i & 7] = (bf16)p;
+          const bf16 dsb = (bf16)ds;
+          db8[i >> 3][i & 7] = dsb;
+          ds4[t] = dsb;
+        }
+        // dS^T row = this lane's key, queries 32qs + 8r + 4hl .. +3.
+        *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, 4 * qs + r) + 4 * hl) = ds4;
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int dbk = 0; dbk < DB; ++dbk) {
+          dv_acc[dbk] = mfma32(gt[dbk][c], pb[c], dv_acc[dbk]);
+          dk_acc[dbk] = mfma32(qt[dbk][c], db8[c], dk_acc[dbk]);
+        }
+    };
     if (!wave_active) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, c) + 4 * hl) = bf16x4{};
+    } else if ((qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || kSeg) {
+      qs_body(0, std::true_type{});
+      qs_body(1, std::true_type{});
     } else {
-      const bool need_mask = (qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || kSeg;
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        bf16x8 qf[KC], gf[KC];
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          qf[kc] = at64::rowfrag(Qs, 32 * qs + l32, 2 * kc + hl);
-          gf[kc] = at64::rowfrag(dOs, 32 * qs + l32, 2 * kc + hl);
-        }
-        f32x16 sacc = f32x16{}, pacc = f32x16{};
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          sacc = mfma32(qf[kc], kreg[kc], sacc);
-          pacc = mfma32(gf[kc], vreg[kc], pacc);
-        }
-        // Transposed operands of dV^T += dO^T P and dK^T += Q^T dS, read while
-        // the softmax below runs on the VALU.
-        bf16x8 gt[DB][2], qt[DB][2];
-#pragma unroll
-        for (int dbk = 0; dbk < DB; ++dbk)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            gt[dbk][c] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
-            qt[dbk][c] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
-          }
-        bf16x8 pb[2], db8[2];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int qr = 32 * qs + 8 * r + 4 * hl;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse_s[qr]);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&delta_s[qr]);
-          bf16x4 ds4;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int i = 4 * r + t;
-            float p = fast_exp2(fmaf(sacc[i], scale_log2, -l4[t]));
-            if (need_mask) {
-              const int q = qq0 + qr + t;
-              bool vis = my_k <= q && q < S && k_ok;
-              if (kSeg && vis) vis = seg_s[qr + t] == seg_k;
-              p = vis ? p : 0.f;
-            }
-            const float ds = p * fmaf(pacc[i], scale, -d4[t]);
-            pb[i >> 3][i & 7] = (bf16)p;
-            const bf16 dsb = (bf16)ds;
-            db8[i >> 3][i & 7] = dsb;
-            ds4[t] = dsb;
-          }
-          // dS^T row = this lane's key, queries 32qs + 8r + 4hl .. +3.
-          *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, 4 * qs + r) + 4 * hl) = ds4;
-        }
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int dbk = 0; dbk < DB; ++dbk) {
-            dv_acc[dbk] = mfma32(gt[dbk][c], pb[c], dv_acc[dbk]);
-            dk_acc[dbk] = mfma32(qt[dbk][c], db8[c], dk_acc[dbk]);
-          }
-      }
+      qs_body(0, std::false_type{});
+      qs_body(1, std::false_type{});
     }
     __syncthreads();  // (B) dS^T published
 
@@ -853,11 +862,18 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
 #pragma unroll
         for (int j = 0; j < 4; ++j) dq = mfma32(af[j], bfk[j], dq);
       }
-      const int dcol = 32 * dblk + l32;
+      // Row q = qq0 + 32qs + 4hl + 8(i/4) + i%4 of this lane's column: one base
+      // address, constant offsets; the bounds test is per block, not per element.
+      float* dq_row = dq_bh + (size_t)(qq0 + 32 * qs + 4 * hl) * D + 32 * dblk + l32;
+      if (qq0 + kBwdM <= S) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int q = qq0 + 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (q < S) atomicAdd(dq_bh + (size_t)q * D + dcol, dq[i]);
+        for (int i = 0; i < 16; ++i) atomicAdd(dq_row + (8 * (i >> 2) + (i & 3)) * D, dq[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int q = qq0 + 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
+          if (q < S) atomicAdd(dq_row + (8 * (i >> 2) + (i & 3)) * D, dq[i]);
+        }
       }
     }
     // The next block's store_q only touches Q/dO (last read before (B)); its

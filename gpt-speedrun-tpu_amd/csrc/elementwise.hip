@@ -138,6 +138,92 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const bf16* __restrict
 
 // out[j] (+)= sum_p partial[p][j]: 64 columns x 4 part-slices per block, the
 // part range split over gridDim.y, one atomic per column per block.
+// Row width a multiple of 8 (at most 2048): one wave per row, 16-byte loads
+// (lane l holds chunks l, l+64, ... of 8 elements), two rows per iteration so
+// the loads of both rows (x, dy and the residual gradient) are in flight
+// before either row's reduction.
+constexpr int kMaxC8 = 4;
+template <int C>
+__global__ void __launch_bounds__(256) rmsnorm_bwd8_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x,
+                                                           const bf16* __restrict__ scale,
+                                                           const float* __restrict__ rstd,
+                                                           const bf16* __restrict__ dres, bf16* __restrict__ dx,
+                                                           float* __restrict__ partial, int rows, int d) {
+  __shared__ float red[4][kMaxC8 * 512];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c8 = d >> 3;
+  float dsc[C][8];
+  bf16x8 sv[C];
+#pragma unroll
+  for (int t = 0; t < C; ++t) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dsc[t][j] = 0.f;
+    const int c = lane + 64 * t;
+    if (c < c8) sv[t] = *reinterpret_cast<const bf16x8*>(scale + 8 * c);
+  }
+  const int stride = gridDim.x * 4;
+  for (int row0 = blockIdx.x * 4 + wave; row0 < rows; row0 += 2 * stride) {
+    bf16x8 xv[2][C], gv[2][C], rv[2][C];
+    float r[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = row0 + u * stride;
+      r[u] = row < rows ? rstd[row] : 0.f;
+#pragma unroll
+      for (int t = 0; t < C; ++t) {
+        const int c = lane + 64 * t;
+        if (row < rows && c < c8) {
+          const size_t o = (size_t)row * d + 8 * c;
+          xv[u][t] = *reinterpret_cast<const bf16x8*>(x + o);
+          gv[u][t] = *reinterpret_cast<const bf16x8*>(dy + o);
+          if (dres) rv[u][t] = *reinterpret_cast<const bf16x8*>(dres + o);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = row0 + u * stride;
+      if (row >= rows) break;  // uniform across the wave
+      float dot = 0.f;
+#pragma unroll
+      for (int t = 0; t < C; ++t)
+        if (lane + 64 * t < c8)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            dot += (float)(bf16)((float)gv[u][t][j] * (float)sv[t][j]) * (float)xv[u][t][j];
+      dot = wave_sum(dot);
+      const float coef = r[u] * r[u] * r[u] * dot / (float)d;
+#pragma unroll
+      for (int t = 0; t < C; ++t) {
+        const int c = lane + 64 * t;
+        if (c < c8) {
+          bf16x8 ov;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float xf = (float)xv[u][t][j], g = (float)gv[u][t][j];
+            const float dn = (float)(bf16)(g * (float)sv[t][j]);
+            float v = (float)(bf16)(r[u] * dn - coef * xf);
+            if (dres) v += (float)rv[u][t][j];
+            ov[j] = (bf16)v;
+            dsc[t][j] += g * (float)(bf16)(xf * r[u]);
+          }
+          *reinterpret_cast<bf16x8*>(dx + (size_t)row * d + 8 * c) = ov;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < C; ++t) {
+    const int c = lane + 64 * t;
+    if (c < c8)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[wave][8 * c + j] = dsc[t][j];
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < d; j += blockDim.x)
+    partial[(size_t)blockIdx.x * d + j] = red[0][j] + red[1][j] + red[2][j] + red[3][j];
+}
+
 __global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict__ partial, int parts, int d,
                                                          float* __restrict__ out) {
   __shared__ float red[4][64];
@@ -282,18 +368,20 @@ __global__ void embedding_fwd_kernel(const int32_t* __restrict__ tok, const bf16
       *reinterpret_cast<const bf16x8*>(table + (size_t)id * d + 8 * c);
 }
 
-__global__ void embedding_bwd_kernel(const int32_t* __restrict__ tok, const bf16* __restrict__ dout,
-                                     float* __restrict__ dtable, int n, int d, int vocab) {
-  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int chunks = d / 8;
-  if (t >= (int64_t)n * chunks) return;
-  int row = (int)(t / chunks), c = (int)(t % chunks);
-  int id = tok[row];
+// One wave per token row; lane l adds elements l, l+64, ...: each atomic
+// instruction covers 64 consecutive floats (two 128-byte lines), not 64
+// scattered 32-byte strides.
+__global__ void __launch_bounds__(256) embedding_bwd_kernel(const int32_t* __restrict__ tok,
+                                                            const bf16* __restrict__ dout,
+                                                            float* __restrict__ dtable, int n, int d, int vocab) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const int id = tok[row];
   if (id < 0 || id >= vocab) return;
-  bf16x8 g = *reinterpret_cast<const bf16x8*>(dout + (size_t)row * d + 8 * c);
-  float* dst = dtable + (size_t)id * d + 8 * c;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) atomicAdd(dst + j, (float)g[j]);
+  const int lane = threadIdx.x & 63;
+  const bf16* src = dout + (size_t)row * d;
+  float* dst = dtable + (size_t)id * d;
+  for (int e = lane; e < d; e += 64) atomicAdd(dst + e, (float)src[e]);
 }
 
 // ----------------------------------------------------------------------------
@@ -451,9 +539,10 @@ int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, i
 }
 
 static int rmsnorm_bwd_blocks(int rows) {
-  // About two rows per wave: enough waves in flight to cover HBM latency.
+  // Eight rows per workgroup pass (two per wave), at most 1024 workgroups:
+  // enough loads in flight to cover HBM latency, and few dscale partials.
   const int b = ceil_div(rows, 8);
-  return b < 1 ? 1 : (b > 4096 ? 4096 : b);
+  return b < 1 ? 1 : (b > 1024 ? 1024 : b);
 }
 
 size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d) {
@@ -473,9 +562,21 @@ int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const f
     fill_f32_kernel<<<ceil_div(d, 256), 256, 0, s>>>(dscale, d, 0.f);
     GPTRIG_CHECK_LAUNCH();
   }
-  rmsnorm_bwd_kernel<<<blocks, 256, 4 * d * sizeof(float), s>>>((const bf16*)dy, (const bf16*)x, (const bf16*)scale,
-                                                                  rstd, (const bf16*)dresidual, (bf16*)dx,
-                                                                  (float*)workspace, rows, d);
+  const int c8 = ceil_div(d / 8, 64);
+  if (d % 8 == 0 && c8 <= kMaxC8) {
+#define GPTRIG_RMS8(C)                                                                                          \
+  rmsnorm_bwd8_kernel<C><<<blocks, 256, 0, s>>>((const bf16*)dy, (const bf16*)x, (const bf16*)scale, rstd,        \
+                                                (const bf16*)dresidual, (bf16*)dx, (float*)workspace, rows, d)
+    if (c8 == 1) GPTRIG_RMS8(1);
+    else if (c8 == 2) GPTRIG_RMS8(2);
+    else if (c8 == 3) GPTRIG_RMS8(3);
+    else GPTRIG_RMS8(4);
+#undef GPTRIG_RMS8
+  } else
+    rmsnorm_bwd_kernel<<<blocks, 256, 4 * d * sizeof(float), s>>>((const bf16*)dy, (const bf16*)x,
+                                                                    (const bf16*)scale, rstd,
+                                                                    (const bf16*)dresidual, (bf16*)dx,
+                                                                    (float*)workspace, rows, d);
   GPTRIG_CHECK_LAUNCH();
   column_sum_kernel<<<dim3(ceil_div(d, 64), 16), 256, 0, s>>>((const float*)workspace, blocks, d, dscale);
   GPTRIG_CHECK_LAUNCH();
@@ -565,8 +666,8 @@ int gptrig_embedding_bwd(const int32_t* tokens, const void* dout, float* dtable,
   if (!tokens || !dout || !dtable) return GPTRIG_E_NULL;
   if (n < 0 || d <= 0 || d % 8 || vocab <= 0) return GPTRIG_E_SHAPE;
   if (n == 0) return GPTRIG_OK;
-  embedding_bwd_kernel<<<ceil_div((long long)n * (d / 8), 256), 256, 0, (hipStream_t)stream>>>(
-      tokens, (const bf16*)dout, dtable, n, d, vocab);
+  embedding_bwd_kernel<<<ceil_div(n, 4), 256, 0, (hipStream_t)stream>>>(tokens, (const bf16*)dout, dtable, n, d,
+                                                                        vocab);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
