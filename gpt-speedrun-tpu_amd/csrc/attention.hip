@@ -27,7 +27,9 @@ namespace {
 
 constexpr int kBlockM = 128;  // forward: queries per workgroup
 constexpr int kBlockN = 64;   // forward: keys per LDS tile
-constexpr int kBwdN = 128;    // backward: keys per workgroup
+constexpr int kBwdN = 128;    // backward (head_dim 128): keys per workgroup
+constexpr int kBwd64Threads = 512;  // backward (head_dim 64): 8 waves of 32 keys
+constexpr int kBwd64Keys = 256;     // backward (head_dim 64): keys per workgroup
 constexpr int kBwdM = 64;     // backward: queries per step
 constexpr float kMinusBig = -1.0e30f;
 
@@ -42,18 +44,17 @@ struct MutView {
   __device__ __forceinline__ bf16* row(int b, int h, int s) const { return p + b * sb + h * sh + s * ss; }
 };
 
-// Workgroup id -> (batch*head, block) such that all blocks of one (b, h) run on
-// the same XCD (workgroups are dispatched round-robin over the 8 XCDs), which
-// keeps that head's K/V (forward) or Q/dO/dQ (backward) in one L2.
+// Workgroup id -> (batch*head, block rank), rank-major: every head's rank-0
+// block (its heaviest causal share, see the callers) is dispatched before any
+// rank-1 block, and so on, so the last workgroups to start are the light ones
+// and the tail stays short.  Workgroups are dispatched round-robin over the 8
+// XCDs; with batch*heads a multiple of 8 all blocks of one head land on the
+// same XCD, which keeps that head's K/V (forward) or Q/dO/dQ (backward) in one
+// L2.
 __device__ __forceinline__ void xcd_map(int id, int nblocks, int bh_total, int& bh, int& blk) {
-  if ((bh_total & 7) == 0) {
-    int xcd = id & 7, slot = id >> 3;
-    bh = (slot / nblocks) * 8 + xcd;
-    blk = slot % nblocks;
-  } else {
-    bh = id / nblocks;
-    blk = id % nblocks;
-  }
+  (void)nblocks;
+  bh = id % bh_total;
+  blk = id / bh_total;
 }
 
 // ============================================================================
@@ -671,30 +672,27 @@ __global__ void __launch_bounds__(256, 2)
 // transposed reads, so nothing is written to LDS transposed.  dS is stored as
 // dS^T [key][query] (8-byte writes) and dQ = dS K is added to an fp32
 // accumulator with atomics.
-#ifndef GPTRIG_BWD64_OCC
-#define GPTRIG_BWD64_OCC 2
-#endif
 template <bool kSeg>
-__global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
+__global__ void __launch_bounds__(kBwd64Threads, 2)
     attn_bwd64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
                       const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
                       MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2) {
-  constexpr int D = 64, KC = 4, DB = 2;
-  __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 128 + 128) * 64];
+  constexpr int D = 64, KC = 4, DB = 2, NT = kBwd64Threads, NK = kBwd64Keys;
+  __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 2 * NK) * 64];
   __shared__ __attribute__((aligned(16))) float lse_s[kBwdM], delta_s[kBwdM];
   __shared__ int seg_s[kBwdM];
   at64::lds_t* const Qs = gemm::lds_cast(smem);
   at64::lds_t* const dOs = Qs + 64 * 64;
   at64::lds_t* const Ks = dOs + 64 * 64;
-  at64::lds_t* const dSt = Ks + 128 * 64;
+  at64::lds_t* const dSt = Ks + NK * 64;
 
-  const int nkv = (S + kBwdN - 1) / kBwdN;
+  const int nkv = (S + NK - 1) / NK;
   int bh, kb;
   xcd_map(blockIdx.x, nkv, B * H, bh, kb);
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
-  const int k0 = kb * kBwdN;
+  const int k0 = kb * NK;
   const int kw0 = k0 + 32 * wave;
   const int my_k = kw0 + l32;
   const bool k_ok = my_k < S;
@@ -707,10 +705,10 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
   }
   const int seg_k = (kSeg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
 
-  // K tile of the workgroup's 128 keys (row-major, swizzled) for dQ = dS K.
+  // K tile of the workgroup's keys (row-major, swizzled) for dQ = dS K.
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int idx = tid + 256 * r;
+    const int idx = tid + NT * r;
     const int row = idx >> 3, c = idx & 7;
     const bf16x8 kv = k0 + row < S ? *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + row) + 8 * c) : bf16x8{};
     *(at64::lds_x8*)(Ks + at64::swz(row, c)) = kv;
@@ -726,14 +724,15 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
   const float* delta_bh = delta + (size_t)bh * S;
   float* dq_bh = dq_acc + (size_t)bh * S * D;
 
-  // Register staging of one 64-query block: 2 x 16 B of Q and of dO per thread.
-  bf16x8 qst[2], gst[2];
+  // Register staging of one 64-query block: 16 B of Q and of dO per thread and step.
+  constexpr int QR = 64 * 8 / NT;
+  bf16x8 qst[QR], gst[QR];
   float lse_st = 0.f, delta_st = 0.f;
   int seg_st = 0;
   auto load_q = [&](int qq0) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int idx = tid + 256 * r;
+    for (int r = 0; r < QR; ++r) {
+      const int idx = tid + NT * r;
       const int qi = idx >> 3, c = idx & 7;
       const bool ok = qq0 + qi < S;
       qst[r] = ok ? *reinterpret_cast<const bf16x8*>(Q.row(b, h, qq0 + qi) + 8 * c) : bf16x8{};
@@ -748,8 +747,8 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
   };
   auto store_q = [&]() {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int idx = tid + 256 * r;
+    for (int r = 0; r < QR; ++r) {
+      const int idx = tid + NT * r;
       const int qi = idx >> 3, c = idx & 7;
       *(at64::lds_x8*)(Qs + at64::swz(qi, c)) = qst[r];
       *(at64::lds_x8*)(dOs + at64::swz(qi, c)) = gst[r];
@@ -764,14 +763,18 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
   const int qb_first = k0 / kBwdM;
   const int nqb = (S + kBwdM - 1) / kBwdM;
   load_q(qb_first * kBwdM);
+  store_q();
 
   for (int qb = qb_first; qb < nqb; ++qb) {
     const int qq0 = qb * kBwdM;
-    store_q();
-    __syncthreads();  // (A) Q, dO, lse, delta of this block published
-    // Unconditional prefetch (the last step re-reads its own block) keeps the
-    // memory-counter state identical on every iteration, so the wait for it is
-    // exact instead of draining the dQ atomics too.
+    // (A) Q, dO, lse, delta of this block published.  Only LDS has to be
+    // complete here: the previous block's dQ atomics stay in flight.
+    GPTRIG_WAIT_LGKM0();
+    wg_barrier();
+    // Prefetch the next block into registers; it is written to LDS after (B),
+    // once every wave is done with this block's Q / dO, ahead of the dQ
+    // atomics (so that wait never drains them).
+    // (The last block re-loads itself: the same code on every iteration.)
     load_q(qb + 1 < nqb ? qq0 + kBwdM : qq0);
 
     const bool wave_active = kw0 <= qq0 + kBwdM - 1 && kw0 < S;
@@ -846,22 +849,26 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
       qs_body(0, std::false_type{});
       qs_body(1, std::false_type{});
     }
-    __syncthreads();  // (B) dS^T published
+    GPTRIG_WAIT_LGKM0();
+    wg_barrier();  // (B) dS^T published; Q / dO / lse / delta of this block no longer read
+    store_q();
 
-    {  // dQ tile of this wave: queries 32*(wave/2).., d 32*(wave%2).. over the 128 keys.
+    if (wave < 4) {  // dQ tile of this wave: queries 32*(wave/2).., d 32*(wave%2).. over all NK keys.
       const int qs = wave >> 1, dblk = wave & 1;
-      f32x16 dq = f32x16{};
+      // Two independent accumulation chains halve the dependent-MFMA latency.
+      f32x16 dqh[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      for (int kq = 0; kq < NK / 64; ++kq) {
         bf16x8 af[4], bfk[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          af[j] = at64::trfrag<false>(dSt, 32 * qs, 16 * (4 * half + j), lane);
-          bfk[j] = at64::trfrag<false>(Ks, 32 * dblk, 16 * (4 * half + j), lane);
+          af[j] = at64::trfrag<false>(dSt, 32 * qs, 16 * (4 * kq + j), lane);
+          bfk[j] = at64::trfrag<false>(Ks, 32 * dblk, 16 * (4 * kq + j), lane);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dq = mfma32(af[j], bfk[j], dq);
+        for (int j = 0; j < 4; ++j) dqh[kq & 1] = mfma32(af[j], bfk[j], dqh[kq & 1]);
       }
+      const f32x16 dq = dqh[0] + dqh[1];
       // Row q = qq0 + 32qs + 4hl + 8(i/4) + i%4 of this lane's column: one base
       // address, constant offsets; the bounds test is per block, not per element.
       float* dq_row = dq_bh + (size_t)(qq0 + 32 * qs + 4 * hl) * D + 32 * dblk + l32;
@@ -876,9 +883,8 @@ __global__ void __launch_bounds__(256, GPTRIG_BWD64_OCC)
         }
       }
     }
-    // The next block's store_q only touches Q/dO (last read before (B)); its
-    // dS^T writes come after the next (A), which every wave reaches only after
-    // finishing this dQ step.
+    // The next block's dS^T writes come after the next (A), which every wave
+    // reaches only after finishing this dQ step.
   }
 
   if (k_ok) {
@@ -992,12 +998,13 @@ int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
     attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
                                                                                 seq);
     GPTRIG_CHECK_LAUNCH();
+    const unsigned grid64 = (unsigned)((long long)batch * heads * ceil_div(seq, kBwd64Keys));
     if (segment_ids)
-      attn_bwd64_kernel<true><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV,
-                                                             batch, heads, seq, softmax_scale, sl2);
+      attn_bwd64_kernel<true><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV,
+                                                               batch, heads, seq, softmax_scale, sl2);
     else
-      attn_bwd64_kernel<false><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, nullptr, dq_acc, dK, dV, batch,
-                                                              heads, seq, softmax_scale, sl2);
+      attn_bwd64_kernel<false><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, nullptr, dq_acc, dK, dV,
+                                                                batch, heads, seq, softmax_scale, sl2);
     GPTRIG_CHECK_LAUNCH();
     attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq);
   } else {

@@ -71,6 +71,19 @@ __device__ __forceinline__ float gelu_grad_f(float x) {
   return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * 0.044715f * x * x);
 }
 
+// Workgroup barrier without the vmcnt(0)/lgkmcnt(0) drain of __syncthreads():
+// the caller issues exactly the s_waitcnt it needs first (gfx950 barriers do
+// not wait for outstanding memory by themselves).  The empty asm statements
+// keep the compiler from moving memory accesses across the barrier, which the
+// bare intrinsic does not.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// s_waitcnt lgkmcnt(0) only (vmcnt and expcnt left at their maxima).
+#define GPTRIG_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
 // Pack 8 floats into an MFMA bf16 operand.
 __device__ __forceinline__ bf16x8 pack8(const float* v) {
   bf16x8 r;

@@ -202,7 +202,7 @@ __device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, 
   if (kColSum && colsum_on) colsum_slab(*colsum, stage_ptr<S>() + OPE, c.tid);
   mma_half(acc, a0, b0);
   GEMM_WAIT_VM8_LGKM0();
-  __builtin_amdgcn_s_barrier();
+  wg_barrier();
   fill(stage_ptr<S>(), c, kt + 4);
   read_half<AK, BKM>(a0, b0, stage_ptr<(S + 1) % 4>(), 0, c);
   mma_half(acc, a1, b1);
@@ -233,7 +233,7 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand
   fill(stage_ptr<2>(), c, 2);
   fill(stage_ptr<3>(), c, 3);
   GEMM_WAIT_VM12_LGKM0();
-  __builtin_amdgcn_s_barrier();
+  wg_barrier();
   bf16x8 a0[4], b0[2];
   read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
   for (int kt = 0; kt < nk; kt += 4) {
