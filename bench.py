@@ -33,6 +33,13 @@ import torch  # noqa: E402
 
 METRIC = "train tokens/s at 125M S=1024; attn-bwd + FLCE TFLOP/s as % of bf16 MFMA peak"
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# HBM bytes of one FLCE fwd+bwd launch sequence at the bench shape (N 32768,
+# d 768, V 50304, three vocabulary chunks): FETCH_SIZE (x 2.0, the factor the
+# counter reads for a 256 MiB copy) + WRITE_SIZE (x 1.0) summed over its
+# launches, from `rocprofv3 --pmc` runs of this tree; the per-launch table and
+# commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
+# changes.
+FLCE_TRAFFIC_BYTES = (20086 + 5951) * 2 ** 20
 
 
 def parse_args():
@@ -183,7 +190,8 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "flce (fused LM-head cross-entropy fwd+bwd, per 32x1024-token micro-batch)",
                      "bound": "mfma", "achieved": round(flce_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(flce_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(flce_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": FLCE_TRAFFIC_BYTES, "traffic_GBps": round(FLCE_TRAFFIC_BYTES / flce_ms / 1e6, 1),
                      "ms": round(flce_ms, 3), "algorithmic_flops": flce_flops(mb_tokens, cfg.d_model,
                                                                               cfg.vocab_size)},
         "roofline_attn_bwd": {"kernel": "attn_bwd (B32 H12 S1024 D64 causal)", "bound": "mfma",

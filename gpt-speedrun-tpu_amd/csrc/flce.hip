@@ -150,10 +150,8 @@ __global__ void __launch_bounds__(gemm::THREADS)
     gemm_f32_kernel(Operand A, Operand B, int M, int N, int K, int ksplit, float* __restrict__ C, int64_t ldc,
                     int mode, float* __restrict__ colsum) {
   __shared__ float red[8 * 256];
-  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int split = blockIdx.x / tiles;
-  int tm, tn;
-  gemm::tile_coords(blockIdx.x % tiles, M, N, tm, tn);
+  int tm, tn, split;
+  gemm::split_tile_coords(blockIdx.x, gridDim.x, M, N, tm, tn, split);
   const int kslice = ((K + ksplit - 1) / ksplit + gemm::BK - 1) / gemm::BK * gemm::BK;
   const int k_begin = split * kslice;
   const int k_end = min(K, k_begin + kslice);
@@ -219,12 +217,14 @@ __global__ void zero_f32_kernel(float* __restrict__ x, int64_t n) {
 
 inline unsigned tiles_of(int M, int N) { return (unsigned)(ceil_div(M, BM) * ceil_div(N, BN)); }
 
-constexpr int kDefaultChunk = 8192;
+// Default vocabulary chunk of the backward: a third of the vocabulary (rounded
+// up to the 256-row tile), so the G^T workspace stays a third of the logits.
+constexpr int kDefaultChunkParts = 3;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int resolve_chunk(int vocab, int vocab_chunk) {
-  int chunk = vocab_chunk <= 0 ? kDefaultChunk : vocab_chunk;
+  int chunk = vocab_chunk <= 0 ? ceil_div(ceil_div(vocab, kDefaultChunkParts), BM) * BM : vocab_chunk;
   const int full = ceil_div(vocab, BM) * BM;
   return chunk > full ? full : chunk;
 }

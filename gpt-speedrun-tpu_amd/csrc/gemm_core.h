@@ -265,6 +265,24 @@ __device__ __forceinline__ void tile_coords(int pid, int M, int N, int& tm, int&
   tn = (pid % in_group) / gsize;
 }
 
+// (tile, K-split) of a split-K launch of tiles x splits workgroups.  The
+// XCD-contiguous logical id runs fastest over the shorter tile dimension, then
+// the longer one, then the split: workgroups that run together on one XCD
+// share the same K range and the same slab of the long operand, so each slab
+// leaves HBM about once instead of once per tile of the short dimension.
+__device__ __forceinline__ void split_tile_coords(int pid, int total, int M, int N, int& tm, int& tn, int& split) {
+  const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+  const int gid = xcd_swizzle(pid, total);
+  if (mt <= nt) {
+    tm = gid % mt;
+    tn = (gid / mt) % nt;
+  } else {
+    tn = gid % nt;
+    tm = (gid / nt) % mt;
+  }
+  split = gid / (mt * nt);
+}
+
 // ---- host side: launch shaping ----
 
 inline int device_cus() {

@@ -281,7 +281,9 @@ class GPTTrainer:
         _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
 
         # ---- backward ----
-        chunk = lce.chunk_for(c.vocab_tile_size if c.vocab_tile_size > 2048 else 8192)
+        # Three vocabulary chunks: the G^T workspace is a third of the logits'
+        # size, and the per-chunk dW GEMM is tall enough to need little K-split.
+        chunk = lce.chunk_for(max(c.vocab_tile_size, -(-c.vocab_size // 3)))
         ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
         dxf = torch.empty((N, d), dtype=BF16, device=self.device)
         with self._timed("flce"):
