@@ -522,6 +522,37 @@ __global__ void __launch_bounds__(256) weighted_sum_kernel(const float* __restri
 
 }  // namespace
 
+// ----------------------------------------------------------------------------
+// bf16 transpose, dst[c][r] = src[r][c]: 64 x 64 tiles through LDS (one
+// padding column), 16-byte loads along src rows, 2-byte stores along dst rows
+// grouped so a wave writes 64 consecutive elements.
+// ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) transpose_bf16_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst,
+                                                             int rows, int cols) {
+  __shared__ bf16 tile[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + 256 * i;  // 512 chunks of 8
+    const int r = idx >> 3, c8 = (idx & 7) * 8;
+    if (r0 + r < rows) {
+      if (c0 + c8 + 8 <= cols) {
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)(r0 + r) * cols + c0 + c8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[r][c8 + j] = v[j];
+      } else {
+        for (int j = 0; j < 8 && c0 + c8 + j < cols; ++j) tile[r][c8 + j] = src[(size_t)(r0 + r) * cols + c0 + c8 + j];
+      }
+    }
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6;
+  for (int c = w; c < 64; c += 4) {
+    if (c0 + c < cols && r0 + lane < rows) dst[(size_t)(c0 + c) * rows + r0 + lane] = tile[lane][c];
+  }
+}
+
 // ============================================================================
 // C ABI
 // ============================================================================
@@ -590,6 +621,16 @@ int gptrig_bias_grad(const void* dy, int rows, int cols, float* db, void* stream
   const int ysplit = (rows + 127) / 128;
   bias_grad_kernel<<<dim3(ceil_div(cols / 8, 64), ysplit), 256, 0, (hipStream_t)stream>>>((const bf16*)dy, rows,
                                                                                           cols, db);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_transpose_bf16(const void* src, void* dst, int rows, int cols, void* stream) {
+  if (!src || !dst) return GPTRIG_E_NULL;
+  if (rows <= 0 || cols <= 0 || cols % 8) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)src) & 15) return GPTRIG_E_SHAPE;
+  transpose_bf16_kernel<<<dim3(ceil_div(cols, 64), ceil_div(rows, 64)), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)src, (bf16*)dst, rows, cols);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_adamw": (I, [P, P, P, P, P, P, P, L, I, F, F, F, I, P, P, P]),
     "gptrig_sq_norm_partials": (I, [P, L, I, P, P]),
     "gptrig_finalize_norm": (I, [P, I, F, P, P, P, F, P, P]),
+    "gptrig_transpose_bf16": (I, [P, P, I, I, P]),
     "gptrig_cast_f32_bf16": (I, [P, P, L, P]),
     "gptrig_weighted_sum": (I, [P, L, F, P, P]),
     "gptrig_fill_f32": (I, [P, L, F, P]),

@@ -157,6 +157,11 @@ int gptrig_sq_norm_partials(const float* x, int64_t n_chunks, int chunk, float* 
 int gptrig_finalize_norm(const float* partials, int parts, float grad_clip, float* norm_out, float* clip_out,
                          const float* loss, float lr, float* history_row, void* stream);
 
+/* bf16 transpose dst [cols, rows] = src [rows, cols]^T (cols a multiple of 8):
+ * the K-major copy of a linear weight (rig/nn.py:55-56), which the forward
+ * GEMM reads faster than the [d_in, d_out] layout. */
+int gptrig_transpose_bf16(const void* src, void* dst, int rows, int cols, void* stream);
+
 /* Small helpers of the step: f32 -> bf16 cast, out += weight * sum(x), fill. */
 int gptrig_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream);
 int gptrig_weighted_sum(const float* x, int64_t n, float weight, float* out, void* stream);

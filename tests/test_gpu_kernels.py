@@ -379,3 +379,15 @@ def test_weight_grad_split_k_gemm(with_bias):
             # Fused bias gradient: column sums of dy over all n rows (every split).
             want_b = dy.double().sum(0) - 0.5
             assert float((db.cpu().double() - want_b).abs().max()) <= 1e-3 * max(1.0, float(want_b.abs().max()))
+
+
+def test_transpose_bf16_bit_exact():
+    from gptrig import _lib
+
+    for rows, cols in ((768, 2304), (3072, 768), (100, 72)):
+        x = randn((rows, cols), 121)
+        xg = x.to(DEV)
+        out = torch.empty((cols, rows), dtype=torch.bfloat16, device=DEV)
+        _lib.call("gptrig_transpose_bf16", xg.data_ptr(), out.data_ptr(), rows, cols, _lib.stream())
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), x.t().contiguous())
