@@ -28,9 +28,9 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
     return x.reshape(-1, x.shape[-1]).contiguous()
 
 
-def rmsnorm_forward(x2: torch.Tensor, scale_bf16: torch.Tensor):
+def rmsnorm_forward(x2: torch.Tensor, scale_bf16: torch.Tensor, out: torch.Tensor | None = None):
     rows, d = x2.shape
-    y = torch.empty_like(x2)
+    y = torch.empty_like(x2) if out is None else out
     rstd = torch.empty(rows, dtype=torch.float32, device=x2.device)
     _lib.call("gptrig_rmsnorm_fwd", x2.data_ptr(), scale_bf16.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, d,
               _lib.stream())
@@ -38,9 +38,9 @@ def rmsnorm_forward(x2: torch.Tensor, scale_bf16: torch.Tensor):
 
 
 def rmsnorm_backward(dy2, x2, scale_bf16, rstd, dscale: torch.Tensor | None = None, accumulate: bool = False,
-                     dresidual: torch.Tensor | None = None):
+                     dresidual: torch.Tensor | None = None, out: torch.Tensor | None = None):
     rows, d = x2.shape
-    dx = torch.empty_like(x2)
+    dx = torch.empty_like(x2) if out is None else out
     if dscale is None:
         dscale = torch.empty(d, dtype=torch.float32, device=x2.device)
         accumulate = False

@@ -206,6 +206,19 @@ class GPTTrainer:
         self.history = torch.zeros((steps, 3), dtype=F32, device=self.device)
         self.loss = torch.zeros(1, dtype=F32, device=self.device)
         self.sq_partials = torch.zeros(self.arena.n_chunks, dtype=F32, device=self.device)
+        # Weight gradients are taken once per step over all micro-batches: each
+        # micro-batch writes the inputs and output-gradients of the block
+        # linears into its rows of these [batch*seq, width] buffers, and the
+        # dW/db GEMMs then run with the whole global batch as their K
+        # dimension (same sums as per-micro-batch accumulation, in a different
+        # fp32 order; four times fewer, four times longer split-K launches).
+        T = config.batch_size * config.seq_len
+        d, f = config.d_model, config.mlp_mult * config.d_model
+        widths = {"qkv": (d, 3 * d), "attn": (d, d), "mlp_up": (d, f), "mlp_down": (f, d)}
+        self.lin_in = [{k: torch.empty((T, a), dtype=BF16, device=self.device) for k, (a, _) in widths.items()}
+                       for _ in range(config.layers)]
+        self.lin_dout = [{k: torch.empty((T, b), dtype=BF16, device=self.device) for k, (_, b) in widths.items()}
+                         for _ in range(config.layers)]
         self.norm = torch.zeros(1, dtype=F32, device=self.device)
         self.clip = torch.ones(1, dtype=F32, device=self.device)
         self.head_path = "output_embedding" if config.embeddings == "untied" else "token_embedding"
@@ -245,11 +258,14 @@ class GPTTrainer:
         return x + (out * self.residual_scale).to(BF16)
 
     # -- forward / backward of one micro-batch --------------------------------------
-    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float) -> None:
+    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float, micro: int) -> None:
         c = self.config
         A = self.arena
         Bm, S = tokens.shape
         N, d, H, D = Bm * S, c.d_model, c.heads, c.head_dim
+        rows = slice(micro * N, (micro + 1) * N)
+        lin_in = [{k: t[rows] for k, t in layer.items()} for layer in self.lin_in]
+        lin_dout = [{k: t[rows] for k, t in layer.items()} for layer in self.lin_dout]
         stream = _lib.stream()
         tok = tokens.reshape(-1).to(torch.int32).contiguous()
         tgt = targets.reshape(-1).to(torch.int32).contiguous()
@@ -267,19 +283,19 @@ class GPTTrainer:
         saved = []
         for i in range(c.layers):
             p = f"blocks/{i}/"
-            xn1, rstd1 = rmsnorm_forward(x, A.w(p + "ln1_scale"))
+            xn1, rstd1 = rmsnorm_forward(x, A.w(p + "ln1_scale"), out=lin_in[i]["qkv"])
             qkv = torch.addmm(A.w(p + "qkv_b"), xn1, A.wt(p + "qkv_w").t())
             rope_inplace(qkv, 3 * d, N, S, 2 * H, D)
-            o = torch.empty((N, d), dtype=BF16, device=self.device)
+            o = lin_in[i]["attn"]
             lse = torch.empty((Bm, H, S), dtype=F32, device=self.device)
             with self._timed("attn_fwd"):
                 _lib.call("gptrig_attn_fwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
                           _lib.ptr(seg), o.data_ptr(), lse.data_ptr(), Bm, H, S, D, attn_strides.data_ptr(),
                           self.scale, stream)
             x1 = self._residual(x, torch.addmm(A.w(p + "attn_b"), o, A.wt(p + "attn_w").t()))
-            xn2, rstd2 = rmsnorm_forward(x1, A.w(p + "ln2_scale"))
+            xn2, rstd2 = rmsnorm_forward(x1, A.w(p + "ln2_scale"), out=lin_in[i]["mlp_up"])
             h = torch.addmm(A.w(p + "mlp_up_b"), xn2, A.wt(p + "mlp_up_w").t())
-            g = torch.empty_like(h)
+            g = lin_in[i]["mlp_down"]
             _lib.call("gptrig_gelu_fwd", h.data_ptr(), g.data_ptr(), h.numel(), stream)
             x2 = self._residual(x1, torch.addmm(A.w(p + "mlp_down_b"), g, A.wt(p + "mlp_down_w").t()))
             saved.append((x, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g))
@@ -305,34 +321,41 @@ class GPTTrainer:
             _lib.call("gptrig_flce_bwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(), None,
                       loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, ws.data_ptr(), ws.numel(),
                       N, d, c.vocab_size, c.semantic_vocab_size, chunk, stream)
-        dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True)
+        unit = self.residual_scale == 1.0
+        top = lin_dout[c.layers - 1]["mlp_down"] if unit else None
+        dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True, out=top)
         attn_ws = self._workspace("attn_bwd", _lib.query("gptrig_attn_bwd_workspace_bytes", Bm, H, S, D))
         for i in reversed(range(c.layers)):
             p = f"blocks/{i}/"
             x_in, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g = saved.pop()
-            dm = dx if self.residual_scale == 1.0 else (dx * self.residual_scale).to(BF16)
-            self._weight_grad(p + "mlp_down", g, dm)
+            if unit:
+                dm = dx  # already written into this layer's down-projection gradient rows
+            else:
+                dm = lin_dout[i]["mlp_down"]
+                dm.copy_((dx * self.residual_scale).to(BF16))
             dg = torch.mm(dm, A.w(p + "mlp_down_w").t())
-            dh = torch.empty_like(dg)
+            dh = lin_dout[i]["mlp_up"]
             _lib.call("gptrig_gelu_bwd", dg.data_ptr(), h.data_ptr(), dh.data_ptr(), dh.numel(), stream)
-            self._weight_grad(p + "mlp_up", xn2, dh)
             dxn2 = torch.mm(dh, A.w(p + "mlp_up_w").t())
             dx1, _ = rmsnorm_backward(dxn2, x1, A.w(p + "ln2_scale"), rstd2, A.grad(p + "ln2_scale"), True,
-                                      dresidual=dx)
-            da = dx1 if self.residual_scale == 1.0 else (dx1 * self.residual_scale).to(BF16)
-            self._weight_grad(p + "attn", o, da)
+                                      dresidual=dx, out=lin_dout[i]["attn"] if unit else None)
+            if unit:
+                da = dx1
+            else:
+                da = lin_dout[i]["attn"]
+                da.copy_((dx1 * self.residual_scale).to(BF16))
             do = torch.mm(da, A.w(p + "attn_w").t())
-            dqkv = torch.empty((N, 3 * d), dtype=BF16, device=self.device)
+            dqkv = lin_dout[i]["qkv"]
             with self._timed("attn_bwd"):
                 _lib.call("gptrig_attn_bwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
                           o.data_ptr(), do.data_ptr(), lse.data_ptr(), _lib.ptr(seg), dqkv.data_ptr(),
                           dqkv[:, d:].data_ptr(), dqkv[:, 2 * d:].data_ptr(), attn_ws.data_ptr(), attn_ws.numel(),
                           Bm, H, S, D, bwd_strides.data_ptr(), self.scale, stream)
             rope_inplace(dqkv, 3 * d, N, S, 2 * H, D, backward=True)
-            self._weight_grad(p + "qkv", xn1, dqkv)
             dxn1 = torch.mm(dqkv, A.w(p + "qkv_w").t())
+            below = lin_dout[i - 1]["mlp_down"] if (unit and i > 0) else None
             dx, _ = rmsnorm_backward(dxn1, x_in, A.w(p + "ln1_scale"), rstd1, A.grad(p + "ln1_scale"), True,
-                                     dresidual=dx1)
+                                     dresidual=dx1, out=below)
         _lib.call("gptrig_embedding_bwd", tok.data_ptr(), dx.data_ptr(), A.grad("token_embedding").data_ptr(), N, d,
                   c.vocab_size, stream)
 
@@ -357,11 +380,17 @@ class GPTTrainer:
         stream = _lib.stream()
         A.g.zero_()
         self.loss.zero_()
+        if tuple(x.shape) != (c.batch_size, c.seq_len) or tuple(y.shape) != (c.batch_size, c.seq_len):
+            raise ValueError(f"train_step takes [batch_size, seq_len] = [{c.batch_size}, {c.seq_len}] tokens, got "
+                             f"{tuple(x.shape)} / {tuple(y.shape)}")
         mb = c.micro_batch_size
         n_micro = x.shape[0] // mb
         weight = 1.0 / (n_micro * mb * x.shape[1])
         for j in range(n_micro):
-            self._forward_backward(x[j * mb:(j + 1) * mb], y[j * mb:(j + 1) * mb], weight)
+            self._forward_backward(x[j * mb:(j + 1) * mb], y[j * mb:(j + 1) * mb], weight, j)
+        for i in range(c.layers):
+            for name in ("qkv", "attn", "mlp_up", "mlp_down"):
+                self._weight_grad(f"blocks/{i}/{name}", self.lin_in[i][name], self.lin_dout[i][name])
         self.step_count += 1
         step = self.step_count
         lr = learning_rate(step, c.optimizer)
