@@ -114,28 +114,45 @@ __global__ void __launch_bounds__(gemm::THREADS)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
+  // The bf16 G^T tile is staged through the (now idle) stage arrays, one
+  // 64-row x 256-column band per array, then written out as 16-byte rows:
+  // the accumulator layout would otherwise need 2-byte stores.
+  wg_barrier();  // every wave is done reading the last stage
+  gemm::lds_t* const band[4] = {gemm::stage_ptr<0>(), gemm::stage_ptr<1>(), gemm::stage_ptr<2>(),
+                                gemm::stage_ptr<3>()};
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    const int n = tn * BN + 64 * wn + 32 * nb + l32;
-    if (n >= N) continue;
-    const int t = targets[n];
+    const int nc = 64 * wn + 32 * nb + l32;  // column within the tile
+    const int n = tn * BN + nc;
+    const bool n_ok = n < N;
+    const int t = n_ok ? targets[n] : -1;
     const bool valid_t = t >= 0 && t < sem_v;
     const float ct = valid_t ? (cot ? cot[n] : cot_scale) : 0.f;
-    const float l2 = lse[n] * GPTRIG_LOG2E;
+    const float l2 = n_ok ? lse[n] * GPTRIG_LOG2E : 0.f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int vl = tm * BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (vl >= Vc) continue;
-        const int v = v0 + vl;
+        const int r = 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);  // row within the tile
+        const int v = v0 + tm * BM + r;
         float g = 0.f;
         if (v < sem_v) {
           const float p = fast_exp2(acc[mb][nb][i] * GPTRIG_LOG2E - l2);
           g = (p - (v == t ? 1.f : 0.f)) * ct;
         }
-        gt[(size_t)vl * N + n] = (bf16)g;
+        band[r >> 6][(r & 63) * 256 + nc] = (bf16)g;
       }
+  }
+  GPTRIG_WAIT_LGKM0();
+  wg_barrier();
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int idx = tid + gemm::THREADS * j;  // 256 rows x 32 chunks of 8
+    const int r = idx >> 5, c = idx & 31;
+    const int vl = tm * BM + r;
+    const int n = tn * BN + 8 * c;
+    if (vl < Vc && n < N)
+      *reinterpret_cast<bf16x8*>(gt + (size_t)vl * N + n) = *(const gemm::lds_x8*)(band[r >> 6] + (r & 63) * 256 + 8 * c);
   }
 }
 
