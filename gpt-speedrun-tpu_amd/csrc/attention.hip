@@ -667,24 +667,27 @@ __global__ void __launch_bounds__(256, 2)
   }
 }
 
-// Backward: KV-owned, 128 keys per workgroup (32 per wave), 64 queries per
-// step.  Q/dO/K tiles are swizzled row-major; Q^T, dO^T, K^T and dS come from
-// transposed reads, so nothing is written to LDS transposed.  dS is stored as
-// dS^T [key][query] (8-byte writes) and dQ = dS K is added to an fp32
-// accumulator with atomics.
+// Backward: KV-owned, 256 keys per workgroup (32 per wave), 64 queries per
+// step.  Q/dO/K/V tiles are swizzled row-major; Q^T, dO^T, K^T and dS come
+// from transposed reads, so nothing is written to LDS transposed.  dS is
+// stored as dS^T [key][query] (8-byte writes) and dQ = dS K is added to an
+// fp32 accumulator with buffer atomics.  The loop body keeps no spills: a
+// scratch reload would make the compiler wait for every outstanding vector
+// memory operation, the previous step's dQ atomics included.
 template <bool kSeg>
 __global__ void __launch_bounds__(kBwd64Threads, 2)
     attn_bwd64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
                       const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
                       MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2) {
   constexpr int D = 64, KC = 4, DB = 2, NT = kBwd64Threads, NK = kBwd64Keys;
-  __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 2 * NK) * 64];
+  __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 3 * NK) * 64];
   __shared__ __attribute__((aligned(16))) float lse_s[kBwdM], delta_s[kBwdM];
   __shared__ int seg_s[kBwdM];
   at64::lds_t* const Qs = gemm::lds_cast(smem);
   at64::lds_t* const dOs = Qs + 64 * 64;
   at64::lds_t* const Ks = dOs + 64 * 64;
   at64::lds_t* const dSt = Ks + NK * 64;
+  at64::lds_t* const Vs = dSt + NK * 64;
 
   const int nkv = (S + NK - 1) / NK;
   int bh, kb;
@@ -697,21 +700,21 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
   const int my_k = kw0 + l32;
   const bool k_ok = my_k < S;
 
-  bf16x8 kreg[KC], vreg[KC];
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    kreg[kc] = k_ok ? *reinterpret_cast<const bf16x8*>(K.row(b, h, my_k) + 16 * kc + 8 * hl) : bf16x8{};
-    vreg[kc] = k_ok ? *reinterpret_cast<const bf16x8*>(V.row(b, h, my_k) + 16 * kc + 8 * hl) : bf16x8{};
-  }
   const int seg_k = (kSeg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
 
-  // K tile of the workgroup's keys (row-major, swizzled) for dQ = dS K.
+  // K and V tiles of the workgroup's keys (row-major, swizzled).  K feeds
+  // dQ = dS K (transposed reads) and, like V, the per-key MFMA operands of
+  // S = Q K^T and dP = dO V^T, which are re-read from LDS every step rather
+  // than held in 32 registers for the whole loop.
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int idx = tid + NT * r;
     const int row = idx >> 3, c = idx & 7;
-    const bf16x8 kv = k0 + row < S ? *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + row) + 8 * c) : bf16x8{};
+    const bool ok = k0 + row < S;
+    const bf16x8 kv = ok ? *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + row) + 8 * c) : bf16x8{};
+    const bf16x8 vv = ok ? *reinterpret_cast<const bf16x8*>(V.row(b, h, k0 + row) + 8 * c) : bf16x8{};
     *(at64::lds_x8*)(Ks + at64::swz(row, c)) = kv;
+    *(at64::lds_x8*)(Vs + at64::swz(row, c)) = vv;
   }
 
   f32x16 dv_acc[DB], dk_acc[DB];
@@ -720,9 +723,15 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
     dv_acc[db] = f32x16{};
     dk_acc[db] = f32x16{};
   }
-  const float* lse_bh = lse + (size_t)bh * S;
-  const float* delta_bh = delta + (size_t)bh * S;
-  float* dq_bh = dq_acc + (size_t)bh * S * D;
+  // Per-(b, h) buffer resources: scalar bases, 32-bit per-lane offsets, and
+  // zeros / dropped writes past the end of the sequence instead of branches.
+  const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(Q.row(b, h, 0), (uint32_t)(S * Q.ss * 2));
+  const __amdgpu_buffer_rsrc_t g_rs = make_rsrc(dO.row(b, h, 0), (uint32_t)(S * dO.ss * 2));
+  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (size_t)bh * S, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t delta_rs = make_rsrc(delta + (size_t)bh * S, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t seg_rs =
+      make_rsrc(kSeg ? (const void*)(seg + (size_t)b * S) : (const void*)lse, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t dq_rs = make_rsrc(dq_acc + (size_t)bh * S * D, (uint32_t)S * D * 4u);
 
   // Register staging of one 64-query block: 16 B of Q and of dO per thread and step.
   constexpr int QR = 64 * 8 / NT;
@@ -734,15 +743,15 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
     for (int r = 0; r < QR; ++r) {
       const int idx = tid + NT * r;
       const int qi = idx >> 3, c = idx & 7;
-      const bool ok = qq0 + qi < S;
-      qst[r] = ok ? *reinterpret_cast<const bf16x8*>(Q.row(b, h, qq0 + qi) + 8 * c) : bf16x8{};
-      gst[r] = ok ? *reinterpret_cast<const bf16x8*>(dO.row(b, h, qq0 + qi) + 8 * c) : bf16x8{};
+      qst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              q_rs, ((qq0 + qi) * (int)Q.ss + 8 * c) * 2, 0, 0));
+      gst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              g_rs, ((qq0 + qi) * (int)dO.ss + 8 * c) * 2, 0, 0));
     }
     if (tid < kBwdM) {
-      const int q = qq0 + tid;
-      lse_st = q < S ? lse_bh[q] * GPTRIG_LOG2E : 0.f;
-      delta_st = q < S ? delta_bh[q] * scale : 0.f;  // pre-scaled: dS = P * (scale*dP - scale*Delta)
-      if (kSeg) seg_st = q < S ? seg[(size_t)b * S + q] : 0;
+      lse_st = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lse_rs, (qq0 + tid) * 4, 0, 0));
+      delta_st = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(delta_rs, (qq0 + tid) * 4, 0, 0));
+      if (kSeg) seg_st = (int)__builtin_amdgcn_raw_buffer_load_b32(seg_rs, (qq0 + tid) * 4, 0, 0);
     }
   };
   auto store_q = [&]() {
@@ -754,8 +763,9 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
       *(at64::lds_x8*)(dOs + at64::swz(qi, c)) = gst[r];
     }
     if (tid < kBwdM) {
-      lse_s[tid] = lse_st;
-      delta_s[tid] = delta_st;
+      // Scaled here, after (B), so the loads are not waited for at issue.
+      lse_s[tid] = lse_st * GPTRIG_LOG2E;
+      delta_s[tid] = delta_st * scale;  // dS = P * (scale*dP - scale*Delta)
       if (kSeg) seg_s[tid] = seg_st;
     }
   };
@@ -792,19 +802,9 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
       f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        sacc = mfma32(qf[kc], kreg[kc], sacc);
-        pacc = mfma32(gf[kc], vreg[kc], pacc);
+        sacc = mfma32(qf[kc], at64::rowfrag(Ks, 32 * wave + l32, 2 * kc + hl), sacc);
+        pacc = mfma32(gf[kc], at64::rowfrag(Vs, 32 * wave + l32, 2 * kc + hl), pacc);
       }
-      // Transposed operands of dV^T += dO^T P and dK^T += Q^T dS, read while
-      // the softmax below runs on the VALU.
-      bf16x8 gt[DB][2], qt[DB][2];
-#pragma unroll
-      for (int dbk = 0; dbk < DB; ++dbk)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          gt[dbk][c] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
-          qt[dbk][c] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
-        }
       bf16x8 pb[2], db8[2];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -831,6 +831,14 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
         // dS^T row = this lane's key, queries 32qs + 8r + 4hl .. +3.
         *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, 4 * qs + r) + 4 * hl) = ds4;
       }
+      bf16x8 gt[DB][2], qt[DB][2];
+#pragma unroll
+      for (int dbk = 0; dbk < DB; ++dbk)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          gt[dbk][c] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
+          qt[dbk][c] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
+        }
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -844,9 +852,11 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
       for (int c = 0; c < 8; ++c) *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, c) + 4 * hl) = bf16x4{};
     } else if ((qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || kSeg) {
       qs_body(0, std::true_type{});
+      __builtin_amdgcn_sched_barrier(0);  // keep the two halves' live ranges apart
       qs_body(1, std::true_type{});
     } else {
       qs_body(0, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
       qs_body(1, std::false_type{});
     }
     GPTRIG_WAIT_LGKM0();
@@ -869,19 +879,12 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
         for (int j = 0; j < 4; ++j) dqh[kq & 1] = mfma32(af[j], bfk[j], dqh[kq & 1]);
       }
       const f32x16 dq = dqh[0] + dqh[1];
-      // Row q = qq0 + 32qs + 4hl + 8(i/4) + i%4 of this lane's column: one base
-      // address, constant offsets; the bounds test is per block, not per element.
-      float* dq_row = dq_bh + (size_t)(qq0 + 32 * qs + 4 * hl) * D + 32 * dblk + l32;
-      if (qq0 + kBwdM <= S) {
+      // Row q = qq0 + 32qs + 4hl + 8(i/4) + i%4 of this lane's column; rows at
+      // or past S fall outside the buffer resource and are dropped.
+      const int voff = ((qq0 + 32 * qs + 4 * hl) * D + 32 * dblk + l32) * 4;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) atomicAdd(dq_row + (8 * (i >> 2) + (i & 3)) * D, dq[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int q = qq0 + 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
-          if (q < S) atomicAdd(dq_row + (8 * (i >> 2) + (i & 3)) * D, dq[i]);
-        }
-      }
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(dq[i], dq_rs, voff + (8 * (i >> 2) + (i & 3)) * D * 4, 0, 0);
     }
     // The next block's dS^T writes come after the next (A), which every wave
     // reaches only after finishing this dQ step.
@@ -998,6 +1001,10 @@ int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
     attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
                                                                                 seq);
     GPTRIG_CHECK_LAUNCH();
+    // The kernel addresses one (b, h) slice of Q / dO / dq_acc through 32-bit
+    // buffer offsets.
+    const long long span = (long long)seq * (Q.ss > dO.ss ? Q.ss : dO.ss) * 2;
+    if (span >= (1ll << 31) || (long long)seq * 64 * 4 >= (1ll << 31)) return GPTRIG_E_SHAPE;
     const unsigned grid64 = (unsigned)((long long)batch * heads * ceil_div(seq, kBwd64Keys));
     if (segment_ids)
       attn_bwd64_kernel<true><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV,

@@ -81,6 +81,16 @@ __device__ __forceinline__ void wg_barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+// Buffer resource over [base, base + bytes) with raw (stride 0) addressing:
+// loads past the end return zeros and stores / atomics past it are dropped,
+// and the base lives in scalar registers, so a per-lane 32-bit offset is all
+// an access needs.  0x00020000 is dword 3 of a gfx9-family descriptor
+// (32-bit data format, no swizzle, no index).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 // s_waitcnt lgkmcnt(0) only (vmcnt and expcnt left at their maxima).
 #define GPTRIG_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
