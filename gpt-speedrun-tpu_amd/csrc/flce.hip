@@ -151,22 +151,26 @@ __global__ void __launch_bounds__(gemm::THREADS)
     const int r = idx >> 5, c = idx & 31;
     const int vl = tm * BM + r;
     const int n = tn * BN + 8 * c;
-    if (vl < Vc && n < N)
-      *reinterpret_cast<bf16x8*>(gt + (size_t)vl * N + n) = *(const gemm::lds_x8*)(band[r >> 6] + (r & 63) * 256 + 8 * c);
+    // Streaming (non-temporal) stores: G^T is read back by the next two
+    // launches, not by this one, so it need not displace the W / h slabs
+    // in L2.
+    if (vl < Vc && n < N) {
+      const bf16x8 g8 = *(const gemm::lds_x8*)(band[r >> 6] + (r & 63) * 256 + 8 * c);
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, g8), reinterpret_cast<u32x4*>(gt + (size_t)vl * N + n));
+    }
   }
 }
 
 // C (fp32, row-major [M][ldc]) = / += / atomic+= A B over K range of this split.
 // mode 0: store, 1: accumulate (read-modify-write), 2: atomic add.
-// colsum (nullable, MN-major B only): colsum[n] atomic+= sum over this split's
-// K range of B(k, n), computed by the workgroups of the first M tile from the
-// B slabs already in LDS (the bias gradient of a linear layer, fused into
-// its weight gradient).
+// colsum (nullable): colsum[n] atomic+= sum over this split's
+// K range of B(k, n), computed from the B fragments already in registers and shared out
+// over the M tiles (the bias gradient of a linear layer, fused into its
+// weight gradient).
 template <bool AK, bool BKM>
 __global__ void __launch_bounds__(gemm::THREADS)
     gemm_f32_kernel(Operand A, Operand B, int M, int N, int K, int ksplit, float* __restrict__ C, int64_t ldc,
                     int mode, float* __restrict__ colsum) {
-  __shared__ float red[8 * 256];
   int tm, tn, split;
   gemm::split_tile_coords(blockIdx.x, gridDim.x, M, N, tm, tn, split);
   const int kslice = ((K + ksplit - 1) / ksplit + gemm::BK - 1) / gemm::BK * gemm::BK;
@@ -174,26 +178,23 @@ __global__ void __launch_bounds__(gemm::THREADS)
   const int k_end = min(K, k_begin + kslice);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   f32x16 acc[4][2];
-  f32x4 csum = f32x4{};
-  const bool do_colsum = !BKM && colsum != nullptr && tm == 0;
-  gemm::mainloop<AK, BKM, !BKM>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, &csum, do_colsum);
+  float csum[2] = {0.f, 0.f};
+  // Every M tile of a (tn, split) sums a share of the B stages, so the
+  // column sums cost each workgroup the same.
+  const bool do_colsum = colsum != nullptr;
+  gemm::mainloop<AK, BKM, true>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, csum,
+                                do_colsum ? (M + BM - 1) / BM : 0, tm);
   if (k_begin >= k_end) return;
-  if (do_colsum) {
-    // Reduce the 8 row groups of each column through LDS.
-    const int n4 = (tid & 63) * 4, grp = tid >> 6;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[grp * 256 + n4 + j] = csum[j];
-    __syncthreads();
-    if (tid < 256) {
-      float t = 0.f;
-#pragma unroll
-      for (int g = 0; g < 8; ++g) t += red[g * 256 + tid];
-      const int n = tn * BN + tid;
-      if (n < N) atomicAdd(colsum + n, t);
-    }
-  }
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
+  if (do_colsum && wm == 0) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const float t = csum[nb] + __shfl_xor(csum[nb], 32);
+      const int n = tn * BN + 64 * wn + 32 * nb + l32;
+      if (hl == 0 && n < N) atomicAdd(colsum + n, t);
+    }
+  }
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int n = tn * BN + 64 * wn + 32 * nb + l32;

@@ -145,19 +145,21 @@ __device__ __forceinline__ bf16x8 frag(const lds_t* slab, int r0, int kc, int la
   }
 }
 
-// Column sums of an MN-major B slab of one stage: thread t adds rows
-// 4(t/64) .. +3 of columns 4(t%64) .. +3 (one 8-byte read per row) into sum.
-__device__ __forceinline__ void colsum_slab(f32x4& sum, const lds_t* slab, int tid) {
-  const int n4 = (tid & 63) * 4, k0 = (tid >> 6) * 4;
+// Column sums of B from the B operand fragments of one stage, already in
+// registers: lane (l32, hl) of fragment nb holds B(k, wn0 + 32nb + l32) for
+// the 8 k of its half of the 16-k chunk, so two v_dot2 against (1, 1) per
+// 4 values add them to sum[nb].  Only waves of the first M half call this (the
+// second half holds the same fragments); the two lane halves are combined by
+// the caller.
+__device__ __forceinline__ void colsum_frags(float* sum, const bf16x8 (&b0)[2], const bf16x8 (&b1)[2]) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
 #pragma unroll
-  for (int k = k0; k < k0 + 4; ++k) {
-    const int off = 8 * ((n4 >> 3) ^ (4 * (k & 3))) + (n4 & 7);
-    const bf16x4 v = *(const lds_x4*)(slab + k * 256 + off);
-    sum[0] += (float)v[0];
-    sum[1] += (float)v[1];
-    sum[2] += (float)v[2];
-    sum[3] += (float)v[3];
-  }
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sum[nb] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{b0[nb][2 * j], b0[nb][2 * j + 1]}, one, sum[nb], false);
+      sum[nb] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{b1[nb][2 * j], b1[nb][2 * j + 1]}, one, sum[nb], false);
+    }
 }
 
 // s_waitcnt immediates (gfx9 layout: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8]).
@@ -196,11 +198,13 @@ __device__ __forceinline__ void fill(lds_t* st, const Ctx& c, int kt) {
 // stage kt+1, runs chunk 1's MFMAs.
 template <bool AK, bool BKM, bool kColSum, int S>
 __device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, bf16x8 (&a0)[4], bf16x8 (&b0)[2],
-                                     f32x4* colsum, bool colsum_on) {
+                                     float* colsum, int colsum_period, int colsum_phase) {
   bf16x8 a1[4], b1[2];
   read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
-  if (kColSum && colsum_on) colsum_slab(*colsum, stage_ptr<S>() + OPE, c.tid);
   mma_half(acc, a0, b0);
+  // After the MFMAs are issued, so the sums run beside them.
+  if (kColSum && colsum_period && kt % colsum_period == colsum_phase && (c.wave & 1) == 0)
+    colsum_frags(colsum, b0, b1);
   GEMM_WAIT_VM8_LGKM0();
   wg_barrier();
   fill(stage_ptr<S>(), c, kt + 4);
@@ -210,15 +214,17 @@ __device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, 
 
 // acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
 // with wm0 = 128*(wave&1), wn0 = 64*(wave>>1); K range [k_begin, k_end).
-// With kColSum (MN-major B only) and colsum_on, colsum also accumulates the
-// column sums of B over the K range (see colsum_slab for the thread mapping).
+// With kColSum and colsum_period > 0, colsum[nb] (two floats per lane) also
+// accumulates, in the waves with wave % 2 == 0, the sums of B(k, tn0 + wn0 +
+// 32nb + lane%32) over this lane half's k of the stages kt of the K range
+// with kt % colsum_period == colsum_phase (see colsum_frags): the workgroups
+// that share a B slab split the sums between them.
 // Uses the four stage arrays; on return no copy into them is in flight, but
 // other waves may still read the last stage: barrier before reusing them.
 template <bool AK, bool BKM, bool kColSum = false>
 __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
-                                         int k_end, int tm0, int tn0, f32x4* colsum = nullptr,
-                                         bool colsum_on = false) {
-  static_assert(!kColSum || !BKM, "column sums need an MN-major B operand");
+                                         int k_end, int tm0, int tn0, float* colsum = nullptr,
+                                         int colsum_period = 0, int colsum_phase = 0) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -237,10 +243,10 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand
   bf16x8 a0[4], b0[2];
   read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
   for (int kt = 0; kt < nk; kt += 4) {
-    step<AK, BKM, kColSum, 0>(acc, c, kt, a0, b0, colsum, colsum_on);
-    if (kt + 1 < nk) step<AK, BKM, kColSum, 1>(acc, c, kt + 1, a0, b0, colsum, colsum_on);
-    if (kt + 2 < nk) step<AK, BKM, kColSum, 2>(acc, c, kt + 2, a0, b0, colsum, colsum_on);
-    if (kt + 3 < nk) step<AK, BKM, kColSum, 3>(acc, c, kt + 3, a0, b0, colsum, colsum_on);
+    step<AK, BKM, kColSum, 0>(acc, c, kt, a0, b0, colsum, colsum_period, colsum_phase);
+    if (kt + 1 < nk) step<AK, BKM, kColSum, 1>(acc, c, kt + 1, a0, b0, colsum, colsum_period, colsum_phase);
+    if (kt + 2 < nk) step<AK, BKM, kColSum, 2>(acc, c, kt + 2, a0, b0, colsum, colsum_period, colsum_phase);
+    if (kt + 3 < nk) step<AK, BKM, kColSum, 3>(acc, c, kt + 3, a0, b0, colsum, colsum_period, colsum_phase);
   }
   GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
 }

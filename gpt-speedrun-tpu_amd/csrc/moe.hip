@@ -228,7 +228,6 @@ __global__ void __launch_bounds__(gemm::THREADS)
     moe_gmm_dw_kernel(const bf16* __restrict__ lhs, int64_t lda,
                       const bf16* __restrict__ dy, int64_t ldy, const int32_t* __restrict__ counts, int E, int K,
                       int N, int split, float* __restrict__ dw, float* __restrict__ db) {
-  __shared__ float red[8 * 256];
   const int tiles = ((K + gemm::BM - 1) / gemm::BM) * ((N + gemm::BN - 1) / gemm::BN);
   const int e = blockIdx.x / (tiles * split);
   const int rem = blockIdx.x % (tiles * split);
@@ -247,10 +246,10 @@ __global__ void __launch_bounds__(gemm::THREADS)
   gemm::Operand B{dy + (int64_t)off * ldy, ldy};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   f32x16 acc[4][2];
-  f32x4 csum = f32x4{};
-  const bool do_colsum = db != nullptr && tm == 0;
-  gemm::mainloop<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, &csum,
-                                     do_colsum);
+  float csum[2] = {0.f, 0.f};
+  const bool do_colsum = db != nullptr;  // shared out over the M tiles
+  gemm::mainloop<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, csum,
+                                     do_colsum ? (K + gemm::BM - 1) / gemm::BM : 0, tm);
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
   float* dwe = dw + (int64_t)e * K * N;
@@ -266,17 +265,12 @@ __global__ void __launch_bounds__(gemm::THREADS)
         if (m < K) atomicAdd(dwe + (int64_t)m * N + n, acc[mb][nb][i]);
       }
   }
-  if (do_colsum) {
-    const int n4 = (tid & 63) * 4, grp = tid >> 6;
+  if (do_colsum && wm == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[grp * 256 + n4 + j] = csum[j];
-    __syncthreads();
-    if (tid < 256) {
-      float t = 0.f;
-#pragma unroll
-      for (int g = 0; g < 8; ++g) t += red[g * 256 + tid];
-      const int n = tn * gemm::BN + tid;
-      if (n < N) atomicAdd(db + (int64_t)e * N + n, t);
+    for (int nb = 0; nb < 2; ++nb) {
+      const float t = csum[nb] + __shfl_xor(csum[nb], 32);
+      const int n = tn * gemm::BN + 64 * wn + 32 * nb + l32;
+      if (hl == 0 && n < N) atomicAdd(db + (int64_t)e * N + n, t);
     }
   }
 }
