@@ -108,7 +108,9 @@ __global__ void __launch_bounds__(gemm::THREADS)
                      const int32_t* __restrict__ targets, const float* __restrict__ lse,
                      const float* __restrict__ cot, float cot_scale, bf16* __restrict__ gt) {
   int tm, tn;
-  gemm::tile_coords(blockIdx.x, Vc, N, tm, tn);
+  // Two vocabulary tiles per token sweep: measured 4% faster for this launch
+  // than groups of 8 (the G^T stores compete with the operand slabs for L2).
+  gemm::tile_coords(blockIdx.x, Vc, N, tm, tn, 2);
   f32x16 acc[4][2];
   gemm::mainloop<true, true>(acc, W, Hd, Vc, N, 0, D, tm * BM, tn * BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -198,13 +198,16 @@ __device__ __forceinline__ void fill(lds_t* st, const Ctx& c, int kt) {
 // stage kt+1, runs chunk 1's MFMAs.
 template <bool AK, bool BKM, bool kColSum, int S>
 __device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, bf16x8 (&a0)[4], bf16x8 (&b0)[2],
-                                     float* colsum, int colsum_period, int colsum_phase) {
+                                     float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
   bf16x8 a1[4], b1[2];
   read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
   mma_half(acc, a0, b0);
   // After the MFMAs are issued, so the sums run beside them.
-  if (kColSum && colsum_period && kt % colsum_period == colsum_phase && (c.wave & 1) == 0)
-    colsum_frags(colsum, b0, b1);
+  // colsum_r = kt % colsum_period, kept as a running count (no division).
+  if (kColSum && colsum_period) {
+    if (colsum_r == colsum_phase && (c.wave & 1) == 0) colsum_frags(colsum, b0, b1);
+    colsum_r = colsum_r + 1 == colsum_period ? 0 : colsum_r + 1;
+  }
   GEMM_WAIT_VM8_LGKM0();
   wg_barrier();
   fill(stage_ptr<S>(), c, kt + 4);
@@ -242,11 +245,12 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand
   wg_barrier();
   bf16x8 a0[4], b0[2];
   read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
+  int colsum_r = 0;
   for (int kt = 0; kt < nk; kt += 4) {
-    step<AK, BKM, kColSum, 0>(acc, c, kt, a0, b0, colsum, colsum_period, colsum_phase);
-    if (kt + 1 < nk) step<AK, BKM, kColSum, 1>(acc, c, kt + 1, a0, b0, colsum, colsum_period, colsum_phase);
-    if (kt + 2 < nk) step<AK, BKM, kColSum, 2>(acc, c, kt + 2, a0, b0, colsum, colsum_period, colsum_phase);
-    if (kt + 3 < nk) step<AK, BKM, kColSum, 3>(acc, c, kt + 3, a0, b0, colsum, colsum_period, colsum_phase);
+    step<AK, BKM, kColSum, 0>(acc, c, kt, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
+    if (kt + 1 < nk) step<AK, BKM, kColSum, 1>(acc, c, kt + 1, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
+    if (kt + 2 < nk) step<AK, BKM, kColSum, 2>(acc, c, kt + 2, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
+    if (kt + 3 < nk) step<AK, BKM, kColSum, 3>(acc, c, kt + 3, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
   }
   GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
 }
@@ -259,14 +263,14 @@ __device__ __forceinline__ int xcd_swizzle(int pid, int total) {
   return x * q + min(x, r) + (pid >> 3);
 }
 
-// Grouped tile order: kGroupM M-tiles share each N sweep so their B slabs stay in L2.
-__device__ __forceinline__ void tile_coords(int pid, int M, int N, int& tm, int& tn) {
+// Grouped tile order: `group_m` M-tiles share each N sweep so their B slabs stay in L2.
+__device__ __forceinline__ void tile_coords(int pid, int M, int N, int& tm, int& tn, int group_m = kGroupM) {
   const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
   pid = xcd_swizzle(pid, mt * nt);
-  const int in_group = kGroupM * nt;
+  const int in_group = group_m * nt;
   const int group = pid / in_group;
-  const int first_m = group * kGroupM;
-  const int gsize = min(mt - first_m, kGroupM);
+  const int first_m = group * group_m;
+  const int gsize = min(mt - first_m, group_m);
   tm = first_m + (pid % in_group) % gsize;
   tn = (pid % in_group) / gsize;
 }
