@@ -487,7 +487,10 @@ __global__ void __launch_bounds__(256, 2)
 }
 
 template <int D>
-__global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView dQ, int B, int H, int S) {
+// rcs / rsn (nullable): RoPE tables [S][D/2]; when given, the bf16 dQ is
+// passed back through the transposed rotation (the RoPE VJP) before the store.
+__global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView dQ, int B, int H, int S,
+                                       const bf16* __restrict__ rcs, const bf16* __restrict__ rsn) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = t / (D / 8);
   const int c = (int)(t % (D / 8));
@@ -498,7 +501,41 @@ __global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView
   f32x4 a = *reinterpret_cast<const f32x4*>(src);
   f32x4 bb = *reinterpret_cast<const f32x4*>(src + 4);
   bf16x8 o = {(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3], (bf16)bb[0], (bf16)bb[1], (bf16)bb[2], (bf16)bb[3]};
+  if (rcs) {
+    const bf16x4 c4 = *reinterpret_cast<const bf16x4*>(rcs + (size_t)s * (D / 2) + 4 * c);
+    const bf16x4 s4 = *reinterpret_cast<const bf16x4*>(rsn + (size_t)s * (D / 2) + 4 * c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x2 r = rope_pair((float)o[2 * j], (float)o[2 * j + 1], (float)c4[j], -(float)s4[j]);
+      o[2 * j] = r[0];
+      o[2 * j + 1] = r[1];
+    }
+  }
   *reinterpret_cast<bf16x8*>(dQ.row(bh / H, bh % H, s) + 8 * c) = o;
+}
+
+// Transposed RoPE rotation, in place, of a strided [B, H, S, D] bf16 view
+// (dK of the head_dim 128 backward): one thread per 8 values.
+__global__ void rope_view_bwd_kernel(MutView X, int B, int H, int S, int D, const bf16* __restrict__ rcs,
+                                     const bf16* __restrict__ rsn) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = D / 8;
+  const int64_t row = t / per_row;
+  const int c = (int)(t % per_row);
+  if (row >= (int64_t)B * H * S) return;
+  const int s = (int)(row % S);
+  const int bh = (int)(row / S);
+  bf16* p = X.row(bh / H, bh % H, s) + 8 * c;
+  bf16x8 o = *reinterpret_cast<const bf16x8*>(p);
+  const bf16x4 c4 = *reinterpret_cast<const bf16x4*>(rcs + (size_t)s * (D / 2) + 4 * c);
+  const bf16x4 s4 = *reinterpret_cast<const bf16x4*>(rsn + (size_t)s * (D / 2) + 4 * c);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16x2 r = rope_pair((float)o[2 * j], (float)o[2 * j + 1], (float)c4[j], -(float)s4[j]);
+    o[2 * j] = r[0];
+    o[2 * j + 1] = r[1];
+  }
+  *reinterpret_cast<bf16x8*>(p) = o;
 }
 
 
@@ -678,7 +715,8 @@ template <bool kSeg>
 __global__ void __launch_bounds__(kBwd64Threads, 2)
     attn_bwd64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
                       const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
-                      MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2) {
+                      MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2,
+                      const bf16* __restrict__ rcs, const bf16* __restrict__ rsn) {
   constexpr int D = 64, KC = 4, DB = 2, NT = kBwd64Threads, NK = kBwd64Keys;
   __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 3 * NK) * 64];
   __shared__ __attribute__((aligned(16))) float lse_s[kBwdM], delta_s[kBwdM];
@@ -903,6 +941,17 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
           v4[t] = (bf16)dv_acc[db][4 * r + t];
           k4[t] = (bf16)dk_acc[db][4 * r + t];
         }
+        if (rcs) {  // RoPE VJP: d = 32db + 8r + 4hl + t, pairs (t, t+1) for t = 0, 2
+          const int j0 = (32 * db + 8 * r + 4 * hl) / 2;
+          const bf16x2 c2 = *reinterpret_cast<const bf16x2*>(rcs + (size_t)my_k * (D / 2) + j0);
+          const bf16x2 s2 = *reinterpret_cast<const bf16x2*>(rsn + (size_t)my_k * (D / 2) + j0);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const bf16x2 rr = rope_pair((float)k4[2 * u], (float)k4[2 * u + 1], (float)c2[u], -(float)s2[u]);
+            k4[2 * u] = rr[0];
+            k4[2 * u + 1] = rr[1];
+          }
+        }
         *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * r + 4 * hl) = v4;
         *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * r + 4 * hl) = k4;
       }
@@ -968,10 +1017,15 @@ size_t gptrig_attn_bwd_workspace_bytes(int batch, int heads, int seq, int head_d
   return delta + rows * head_dim * sizeof(float);
 }
 
-int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
-                    const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace,
-                    size_t workspace_bytes, int batch, int heads, int seq, int head_dim, const int64_t* strides,
-                    float softmax_scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The backward launches; rcs / rsn (nullable) add the RoPE VJP to dq and dk.
+int attn_bwd_impl(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                  const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                  int batch, int heads, int seq, int head_dim, const int64_t* strides, float softmax_scale,
+                  const bf16* rcs, const bf16* rsn, void* stream) {
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !workspace) return GPTRIG_E_NULL;
   if (batch <= 0 || heads <= 0 || seq <= 0 || head_dim <= 0) return GPTRIG_E_SHAPE;
   if (head_dim != 64 && head_dim != 128) return GPTRIG_E_UNSUPPORTED;
@@ -998,22 +1052,23 @@ int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
   const long long grid = (long long)batch * heads * nkv;
   const float sl2 = softmax_scale * GPTRIG_LOG2E;
   if (head_dim == 64) {
-    attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
-                                                                                seq);
-    GPTRIG_CHECK_LAUNCH();
     // The kernel addresses one (b, h) slice of Q / dO / dq_acc through 32-bit
     // buffer offsets.
     const long long span = (long long)seq * (Q.ss > dO.ss ? Q.ss : dO.ss) * 2;
     if (span >= (1ll << 31) || (long long)seq * 64 * 4 >= (1ll << 31)) return GPTRIG_E_SHAPE;
+    attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
+                                                                                seq);
+    GPTRIG_CHECK_LAUNCH();
     const unsigned grid64 = (unsigned)((long long)batch * heads * ceil_div(seq, kBwd64Keys));
     if (segment_ids)
       attn_bwd64_kernel<true><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV,
-                                                               batch, heads, seq, softmax_scale, sl2);
+                                                               batch, heads, seq, softmax_scale, sl2, rcs, rsn);
     else
       attn_bwd64_kernel<false><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, nullptr, dq_acc, dK, dV,
-                                                                batch, heads, seq, softmax_scale, sl2);
+                                                                batch, heads, seq, softmax_scale, sl2, rcs, rsn);
     GPTRIG_CHECK_LAUNCH();
-    attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq);
+    attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq,
+                                                                                   rcs, rsn);
   } else {
     attn_bwd_pre_kernel<128><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
                                                                                  seq);
@@ -1021,10 +1076,38 @@ int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
     attn_bwd_kernel<128><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV, batch,
                                                         heads, seq, softmax_scale, sl2);
     GPTRIG_CHECK_LAUNCH();
-    attn_dq_convert_kernel<128><<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq);
+    attn_dq_convert_kernel<128><<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq,
+                                                                                    rcs, rsn);
+    if (rcs) {
+      GPTRIG_CHECK_LAUNCH();
+      rope_view_bwd_kernel<<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(dK, batch, heads, seq, head_dim, rcs,
+                                                                               rsn);
+    }
   }
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                    const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace,
+                    size_t workspace_bytes, int batch, int heads, int seq, int head_dim, const int64_t* strides,
+                    float softmax_scale, void* stream) {
+  return attn_bwd_impl(q, k, v, o, dout, lse, segment_ids, dq, dk, dv, workspace, workspace_bytes, batch, heads, seq,
+                       head_dim, strides, softmax_scale, nullptr, nullptr, stream);
+}
+
+int gptrig_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace,
+                         size_t workspace_bytes, int batch, int heads, int seq, int head_dim, const int64_t* strides,
+                         float softmax_scale, const void* rope_cos, const void* rope_sin, void* stream) {
+  if (!rope_cos || !rope_sin) return GPTRIG_E_NULL;
+  if (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 7) return GPTRIG_E_SHAPE;
+  return attn_bwd_impl(q, k, v, o, dout, lse, segment_ids, dq, dk, dv, workspace, workspace_bytes, batch, heads, seq,
+                       head_dim, strides, softmax_scale, (const bf16*)rope_cos, (const bf16*)rope_sin, stream);
 }
 
 }  // extern "C"

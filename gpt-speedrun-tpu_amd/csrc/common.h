@@ -91,6 +91,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// One interleaved RoPE pair (rig/nn.py:36-52): (e, o) -> (e c - o s, e s + o c)
+// in fp32, each result rounded to bf16.  The backward (transposed) rotation is
+// the same with -s.  Shared by the RoPE pass and the epilogues that fuse it, so
+// both round identically.
+__device__ __forceinline__ bf16x2 rope_pair(float e, float o, float c, float s) {
+  // Explicit fused forms, so every call site rounds the same way.
+  return bf16x2{(bf16)__builtin_fmaf(e, c, -(o * s)), (bf16)__builtin_fmaf(e, s, o * c)};
+}
+
 // s_waitcnt lgkmcnt(0) only (vmcnt and expcnt left at their maxima).
 #define GPTRIG_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 

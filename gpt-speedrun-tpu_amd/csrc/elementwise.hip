@@ -25,9 +25,14 @@ __global__ void fill_f32_kernel(float* __restrict__ x, int64_t n, float value) {
 // ----------------------------------------------------------------------------
 constexpr int kMaxChunks = 8;
 
-__global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ scale,
+// kAdd: the row is first formed as sum = bf16(x + bf16(branch * branch_scale))
+// (the residual add in front of the norm) and written to sum_out, which may
+// be x itself (each lane reads its chunks before writing them).
+template <bool kAdd>
+__global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* x, const bf16* __restrict__ scale,
                                                           bf16* __restrict__ y, float* __restrict__ rstd, int rows,
-                                                          int d) {
+                                                          int d, const bf16* __restrict__ branch, float branch_scale,
+                                                          bf16* sum_out) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;
@@ -41,6 +46,12 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* __restrict
     const int c = lane + kWave * t;
     if (c < chunks) {
       xv[t] = *reinterpret_cast<const bf16x4*>(xr + 4 * c);
+      if (kAdd) {
+        const bf16x4 bv = *reinterpret_cast<const bf16x4*>(branch + (size_t)row * d + 4 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[t][j] = (bf16)((float)xv[t][j] + (float)(bf16)((float)bv[j] * branch_scale));
+        *reinterpret_cast<bf16x4*>(sum_out + (size_t)row * d + 4 * c) = xv[t];
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) ss += (float)xv[t][j] * (float)xv[t][j];
     }
@@ -344,11 +355,11 @@ __global__ void rope_kernel(bf16* __restrict__ x, int64_t row_stride, int rows, 
   bf16x8 o;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float e = (float)v[2 * j], od = (float)v[2 * j + 1];
-    float c = (float)c4[j], s = (float)s4[j];
+    float s = (float)s4[j];
     if (kBackward) s = -s;
-    o[2 * j] = (bf16)(e * c - od * s);
-    o[2 * j + 1] = (bf16)(e * s + od * c);
+    const bf16x2 r = rope_pair((float)v[2 * j], (float)v[2 * j + 1], (float)c4[j], s);
+    o[2 * j] = r[0];
+    o[2 * j + 1] = r[1];
   }
   *reinterpret_cast<bf16x8*>(p) = o;
 }
@@ -563,8 +574,21 @@ int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, i
   if (rows < 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
   if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
   if (rows == 0) return GPTRIG_OK;
-  rmsnorm_fwd_kernel<<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>((const bf16*)x, (const bf16*)scale,
-                                                                          (bf16*)y, rstd, rows, d);
+  rmsnorm_fwd_kernel<false><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, nullptr, 1.0f, nullptr);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_add_rmsnorm_fwd(const void* x, const void* branch, float branch_scale, const void* scale, void* sum,
+                           void* y, float* rstd, int rows, int d, void* stream) {
+  if (!x || !branch || !scale || !sum || !y) return GPTRIG_E_NULL;
+  if (rows < 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
+  if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
+  if (y == x || y == sum || y == branch || sum == branch) return GPTRIG_E_SHAPE;
+  if (rows == 0) return GPTRIG_OK;
+  rmsnorm_fwd_kernel<true><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, (const bf16*)branch, branch_scale, (bf16*)sum);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

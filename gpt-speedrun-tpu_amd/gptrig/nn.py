@@ -37,6 +37,20 @@ def rmsnorm_forward(x2: torch.Tensor, scale_bf16: torch.Tensor, out: torch.Tenso
     return y, rstd
 
 
+def add_rmsnorm_forward(x2: torch.Tensor, branch: torch.Tensor, branch_scale: float, scale_bf16: torch.Tensor,
+                        sum_out: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """``s = x + bf16(branch * branch_scale)`` then ``rms_norm(s)``: the block's
+    residual add and the norm after it in one pass.  Returns ``(s, y, rstd)``."""
+
+    rows, d = x2.shape
+    s = torch.empty_like(x2) if sum_out is None else sum_out
+    y = torch.empty_like(x2) if out is None else out
+    rstd = torch.empty(rows, dtype=torch.float32, device=x2.device)
+    _lib.call("gptrig_add_rmsnorm_fwd", x2.data_ptr(), branch.data_ptr(), float(branch_scale), scale_bf16.data_ptr(),
+              s.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, d, _lib.stream())
+    return s, y, rstd
+
+
 def rmsnorm_backward(dy2, x2, scale_bf16, rstd, dscale: torch.Tensor | None = None, accumulate: bool = False,
                      dresidual: torch.Tensor | None = None, out: torch.Tensor | None = None):
     rows, d = x2.shape

@@ -34,7 +34,7 @@ import torch
 from . import _lib
 from .attention import attention_softmax_scale, document_segments
 from .kernels import linear_cross_entropy as lce
-from .nn import normal, rmsnorm_backward, rmsnorm_forward, rope_inplace
+from .nn import add_rmsnorm_forward, normal, rmsnorm_backward, rmsnorm_forward, rope_inplace, rope_tables
 from .optim import OptimizerConfig, effective_adam_betas, learning_rate, tensor_hparams
 
 BF16 = torch.bfloat16
@@ -252,11 +252,6 @@ class GPTTrainer:
 
         return _Ctx()
 
-    def _residual(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
-        if self.residual_scale == 1.0:
-            return x + out
-        return x + (out * self.residual_scale).to(BF16)
-
     # -- forward / backward of one micro-batch --------------------------------------
     def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float, micro: int) -> None:
         c = self.config
@@ -281,9 +276,14 @@ class GPTTrainer:
         bwd_strides = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o, *st_o, *st_qkv, *st_qkv, *st_qkv],
                                    dtype=torch.int64)
         saved = []
+        # Each residual add runs fused with the norm after it (ln2 of the same
+        # block, ln1 of the next, or the final norm).
+        if c.layers == 0:
+            xf, rstdf = rmsnorm_forward(x, A.w("final_ln_scale"))
+        else:
+            xn1, rstd1 = rmsnorm_forward(x, A.w("blocks/0/ln1_scale"), out=lin_in[0]["qkv"])
         for i in range(c.layers):
             p = f"blocks/{i}/"
-            xn1, rstd1 = rmsnorm_forward(x, A.w(p + "ln1_scale"), out=lin_in[i]["qkv"])
             qkv = torch.addmm(A.w(p + "qkv_b"), xn1, A.wt(p + "qkv_w").t())
             rope_inplace(qkv, 3 * d, N, S, 2 * H, D)
             o = lin_in[i]["attn"]
@@ -292,15 +292,22 @@ class GPTTrainer:
                 _lib.call("gptrig_attn_fwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
                           _lib.ptr(seg), o.data_ptr(), lse.data_ptr(), Bm, H, S, D, attn_strides.data_ptr(),
                           self.scale, stream)
-            x1 = self._residual(x, torch.addmm(A.w(p + "attn_b"), o, A.wt(p + "attn_w").t()))
-            xn2, rstd2 = rmsnorm_forward(x1, A.w(p + "ln2_scale"), out=lin_in[i]["mlp_up"])
+            x1, xn2, rstd2 = add_rmsnorm_forward(x, torch.addmm(A.w(p + "attn_b"), o, A.wt(p + "attn_w").t()),
+                                                 self.residual_scale, A.w(p + "ln2_scale"), out=lin_in[i]["mlp_up"])
             h = torch.addmm(A.w(p + "mlp_up_b"), xn2, A.wt(p + "mlp_up_w").t())
             g = lin_in[i]["mlp_down"]
             _lib.call("gptrig_gelu_fwd", h.data_ptr(), g.data_ptr(), h.numel(), stream)
-            x2 = self._residual(x1, torch.addmm(A.w(p + "mlp_down_b"), g, A.wt(p + "mlp_down_w").t()))
+            down = torch.addmm(A.w(p + "mlp_down_b"), g, A.wt(p + "mlp_down_w").t())
+            if i + 1 < c.layers:
+                x2, xn1_next, rstd1_next = add_rmsnorm_forward(x1, down, self.residual_scale,
+                                                               A.w(f"blocks/{i + 1}/ln1_scale"),
+                                                               out=lin_in[i + 1]["qkv"])
+            else:
+                x2, xf, rstdf = add_rmsnorm_forward(x1, down, self.residual_scale, A.w("final_ln_scale"))
             saved.append((x, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g))
             x = x2
-        xf, rstdf = rmsnorm_forward(x, A.w("final_ln_scale"))
+            if i + 1 < c.layers:
+                xn1, rstd1 = xn1_next, rstd1_next
         head = A.w(self.head_path)
         losses = torch.empty(N, dtype=F32, device=self.device)
         lse_ce = torch.empty(N, dtype=F32, device=self.device)
@@ -325,6 +332,7 @@ class GPTTrainer:
         top = lin_dout[c.layers - 1]["mlp_down"] if unit else None
         dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True, out=top)
         attn_ws = self._workspace("attn_bwd", _lib.query("gptrig_attn_bwd_workspace_bytes", Bm, H, S, D))
+        rope_c, rope_s = rope_tables(S, D, self.device)
         for i in reversed(range(c.layers)):
             p = f"blocks/{i}/"
             x_in, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g = saved.pop()
@@ -346,12 +354,14 @@ class GPTTrainer:
                 da.copy_((dx1 * self.residual_scale).to(BF16))
             do = torch.mm(da, A.w(p + "attn_w").t())
             dqkv = lin_dout[i]["qkv"]
+            # Attention backward with the RoPE VJP of q and k fused into its
+            # dq / dk epilogues.
             with self._timed("attn_bwd"):
-                _lib.call("gptrig_attn_bwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
+                _lib.call("gptrig_attn_bwd_rope", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
                           o.data_ptr(), do.data_ptr(), lse.data_ptr(), _lib.ptr(seg), dqkv.data_ptr(),
                           dqkv[:, d:].data_ptr(), dqkv[:, 2 * d:].data_ptr(), attn_ws.data_ptr(), attn_ws.numel(),
-                          Bm, H, S, D, bwd_strides.data_ptr(), self.scale, stream)
-            rope_inplace(dqkv, 3 * d, N, S, 2 * H, D, backward=True)
+                          Bm, H, S, D, bwd_strides.data_ptr(), self.scale, rope_c.data_ptr(), rope_s.data_ptr(),
+                          stream)
             dxn1 = torch.mm(dqkv, A.w(p + "qkv_w").t())
             below = lin_dout[i - 1]["mlp_down"] if (unit and i > 0) else None
             dx, _ = rmsnorm_backward(dxn1, x_in, A.w(p + "ln1_scale"), rstd1, A.grad(p + "ln1_scale"), True,

@@ -64,6 +64,19 @@ int gptrig_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
                     size_t workspace_bytes, int batch, int heads, int seq, int head_dim,
                     const int64_t* strides /* q,k,v,o,dout,dq,dk,dv */, float softmax_scale, void* stream);
 
+/* The same backward followed by the VJP of the RoPE the block applies to q and
+ * k before attention (recipes/reference/train.py:1141-1142, apply_rotary =
+ * rig/nn.py:36-52): q and k are the rotated tensors the forward saw; dq and dk
+ * come back as the cotangents of the unrotated ones, each first rounded to
+ * bf16 and then rotated by -angle, as gptrig_rope_bwd would do in a second
+ * pass.  rope_cos / rope_sin: the bf16 [seq, head_dim/2] tables of
+ * gptrig_rope_table, 8-byte aligned. */
+int gptrig_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, const int32_t* segment_ids, void* dq, void* dk, void* dv, void* workspace,
+                         size_t workspace_bytes, int batch, int heads, int seq, int head_dim,
+                         const int64_t* strides /* q,k,v,o,dout,dq,dk,dv */, float softmax_scale,
+                         const void* rope_cos, const void* rope_sin, void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused linear cross-entropy (LM head + online log-sum-exp + loss + dh/dW).
  * Replaces rig/kernels/linear_cross_entropy.py:
@@ -96,6 +109,13 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
  * x, y bf16 [rows, d]; scale bf16 [d]; rstd f32 [rows] (saved for backward).
  * ---------------------------------------------------------------------- */
 int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, int rows, int d, void* stream);
+/* The block's residual add fused with the norm that follows it
+ * (recipes/reference/train.py:1164-1169 and :1172-1176: x = residual +
+ * s * linear(...), then rms_norm(x)): sum bf16 [rows, d] =
+ * bf16(x + bf16(branch * branch_scale)), then y, rstd = gptrig_rmsnorm_fwd(sum).
+ * sum may be x (in place); y must not alias x, branch or sum. */
+int gptrig_add_rmsnorm_fwd(const void* x, const void* branch, float branch_scale, const void* scale, void* sum,
+                           void* y, float* rstd, int rows, int d, void* stream);
 size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d);
 /* dx bf16 = d rms_norm/dx (+ dresidual if non-NULL); dscale f32 [d] (+= if accumulate). */
 int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const float* rstd, const void* dresidual,

@@ -227,6 +227,31 @@ def test_rmsnorm_forward_backward():
     assert maxabs(sg.grad, sr.grad) <= 1e-2 * float(sr.grad.abs().max())
 
 
+@pytest.mark.parametrize("branch_scale", [1.0, 0.5 ** 0.5])
+def test_add_rmsnorm_matches_add_then_norm(branch_scale):
+    """The fused residual add + norm equals the oracle's residual add
+    (recipes/reference/train.py:1164) followed by its rms_norm, bit for bit,
+    in place and out of place."""
+    from gptrig import nn as gnn
+
+    x = randn((333, 768), 54, 2.0)
+    br = randn((333, 768), 55, 1.0)
+    scale = (1.0 + 0.1 * randn((768,), 56, 1.0, torch.float32))
+    s_ref = (x.float() + (br.float() * float(np.float32(branch_scale))).to(torch.bfloat16).float()).to(torch.bfloat16)
+    y_ref = onn.rms_norm(s_ref, scale, torch.bfloat16)
+    sc = scale.to(torch.bfloat16).to(DEV)
+    xd, bd = x.to(DEV), br.to(DEV)
+    s, y, rstd = gnn.add_rmsnorm_forward(xd, bd, branch_scale, sc)
+    assert torch.equal(s.cpu(), s_ref)
+    y2, rstd2 = gnn.rmsnorm_forward(s, sc)
+    assert torch.equal(y, y2) and torch.equal(rstd, rstd2)
+    assert maxabs(y, y_ref) <= 2 ** -7 * float(y_ref.float().abs().max())
+    xi = xd.clone()
+    s3, y3, _ = gnn.add_rmsnorm_forward(xi, bd, branch_scale, sc, sum_out=xi)
+    assert s3.data_ptr() == xi.data_ptr()
+    assert torch.equal(xi, s) and torch.equal(y3, y)
+
+
 def test_gelu_forward_backward():
     from gptrig import nn as gnn
 
@@ -252,6 +277,66 @@ def test_rope_forward_backward():
     xg = x.to(DEV).requires_grad_(True)
     gnn.apply_rotary(xg).backward(dy.to(DEV))
     assert maxabs(xg.grad, onn.apply_rotary_backward(dy)) <= 2e-2
+
+
+@pytest.mark.parametrize("D,segmented", [(64, False), (64, True), (128, False)])
+def test_attention_backward_with_rope_vjp_equals_two_passes(D, segmented):
+    """gptrig_attn_bwd_rope == gptrig_attn_bwd followed by gptrig_rope_bwd on
+    dq and dk, bit for bit, on the training step's interleaved qkv layout; and
+    the RoPE'd attention gradient matches the oracle's autograd through
+    apply_rotary and attention."""
+    from gptrig import _lib
+    from gptrig import nn as gnn
+
+    print(f"attention+rope backward D={D} seg={segmented}", flush=True)
+    B, H, S = 2, 3, 320
+    N, d = B * S, H * D
+    qkv0 = randn((N, 3 * d), 91)
+    do = randn((N, d), 92)
+    seg = segments_from_cuts(B, S, (0, 100, 101, 250)) if segmented else None
+    qkv = qkv0.to(DEV)
+    gnn.rope_inplace(qkv, 3 * d, N, S, 2 * H, D)
+    st_qkv, st_o = (S * 3 * d, D, 3 * d), (S * d, D, d)
+    fst = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o], dtype=torch.int64)
+    bst = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o, *st_o, *st_qkv, *st_qkv, *st_qkv], dtype=torch.int64)
+    segg = None if seg is None else seg.to(DEV).contiguous()
+    o = torch.empty((N, d), dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=DEV)
+    sc = D ** -0.5
+    s = _lib.stream()
+    _lib.call("gptrig_attn_fwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(), _lib.ptr(segg),
+              o.data_ptr(), lse.data_ptr(), B, H, S, D, fst.data_ptr(), sc, s)
+    dog = do.to(DEV)
+    ws = torch.empty(_lib.query("gptrig_attn_bwd_workspace_bytes", B, H, S, D), dtype=torch.uint8, device=DEV)
+    outs = []
+    for fused in (False, True):
+        dqkv = torch.zeros((N, 3 * d), dtype=torch.bfloat16, device=DEV)
+        args = [qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(), o.data_ptr(), dog.data_ptr(),
+                lse.data_ptr(), _lib.ptr(segg), dqkv.data_ptr(), dqkv[:, d:].data_ptr(), dqkv[:, 2 * d:].data_ptr(),
+                ws.data_ptr(), ws.numel(), B, H, S, D, bst.data_ptr(), sc]
+        if fused:
+            c, sn = gnn.rope_tables(S, D, qkv.device)
+            _lib.call("gptrig_attn_bwd_rope", *args, c.data_ptr(), sn.data_ptr(), s)
+        else:
+            _lib.call("gptrig_attn_bwd", *args, s)
+            gnn.rope_inplace(dqkv, 3 * d, N, S, 2 * H, D, backward=True)
+        outs.append(dqkv)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    # Against the oracle: attention backward on the rotated q / k (BHSD), then
+    # the transposed rotation of dq / dk (BTHD), as the reference's autodiff
+    # through apply_rotary composes them.
+    x = qkv0.reshape(B, S, 3, H, D)
+    q = onn.apply_rotary(x[:, :, 0]).permute(0, 2, 1, 3)
+    k = onn.apply_rotary(x[:, :, 1]).permute(0, 2, 1, 3)
+    v = x[:, :, 2].permute(0, 2, 1, 3)
+    o_ref, lse_ref = oattn.attention_forward(q, k, v, softmax_scale=sc, segment_ids=seg)
+    dq_r, dk_r, dv_r = oattn.attention_backward(q, k, v, o_ref, lse_ref, do.reshape(B, S, H, D).permute(0, 2, 1, 3),
+                                                softmax_scale=sc, segment_ids=seg)
+    dq_r = onn.apply_rotary_backward(dq_r.permute(0, 2, 1, 3))
+    dk_r = onn.apply_rotary_backward(dk_r.permute(0, 2, 1, 3))
+    want = torch.stack((dq_r, dk_r, dv_r.permute(0, 2, 1, 3)), dim=2).reshape(N, 3 * d)
+    assert maxabs(outs[1], want) <= 2e-2
 
 
 def test_adamw_matches_oracle():
