@@ -50,7 +50,36 @@ def parse_args():
     ap.add_argument("--micro-batch", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="approximate CPU-baseline budget")
+    ap.add_argument("--traffic-pass", action="store_true",
+                    help="run one 256 MiB calibration copy, one FLCE forward+backward and one attention "
+                         "forward+backward at the bench shapes, and exit (the program profiled by the "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     return ap.parse_args()
+
+
+def traffic_pass() -> None:
+    """One launch sequence of each hand-written hot path, for HBM-counter runs."""
+
+    from gptrig.kernels import flash_attention as fa
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    dev = "cuda:0"
+    torch.manual_seed(0)
+    src = torch.randn(64 * 1024 * 1024, device=dev)  # 256 MiB: calibrates the counters
+    torch.empty_like(src).copy_(src)
+    torch.cuda.synchronize()
+    n, d, vocab = 32768, 768, 50304
+    h = torch.randn(n, d, device=dev).bfloat16()
+    w = (torch.randn(vocab, d, device=dev) * 0.02).bfloat16()
+    t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32)
+    _, lse = lce.flce_forward(h, w, t, vocab)
+    lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.chunk_for(-(-vocab // 3)))
+    torch.cuda.synchronize()
+    q, k, v, do = (torch.randn(32, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
+    o, lse2 = fa.flash_forward(q, k, v, None, 0.125)
+    fa.flash_backward(q, k, v, o, lse2, do, None, 0.125)
+    torch.cuda.synchronize()
+    print("traffic pass done", flush=True)
 
 
 def attn_bwd_flops(batch, heads, seq, head_dim):
@@ -115,6 +144,9 @@ def cpu_baseline(seconds: float) -> dict:
 
 def main():
     args = parse_args()
+    if args.traffic_pass:
+        traffic_pass()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU (--gpus > 1) is not implemented",
                           "n_gpus": args.gpus}))

@@ -721,6 +721,9 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
   __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 3 * NK) * 64];
   __shared__ __attribute__((aligned(16))) float lse_s[kBwdM], delta_s[kBwdM];
   __shared__ int seg_s[kBwdM];
+  // RoPE tables (cos, sin) of the workgroup's keys, read by the dK epilogue
+  // when the RoPE VJP is fused; staged here so their loads overlap the loop.
+  __shared__ __attribute__((aligned(16))) bf16 rope_s[2][NK * (D / 2)];
   at64::lds_t* const Qs = gemm::lds_cast(smem);
   at64::lds_t* const dOs = Qs + 64 * 64;
   at64::lds_t* const Ks = dOs + 64 * 64;
@@ -740,6 +743,19 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
 
   const int seg_k = (kSeg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
 
+  {
+    // (Branch-free, so these loads issue together with the K / V loads below.)
+    constexpr int kChunks = NK * (D / 2) / 8;  // 16-byte chunks per table
+#pragma unroll
+    for (int r = 0; r < kChunks / NT; ++r) {
+      const int idx = tid + NT * r;
+      const int key = idx / (D / 16), c = idx % (D / 16);
+      const bool ok = rcs != nullptr && k0 + key < S;
+      const size_t off = ok ? (size_t)(k0 + key) * (D / 2) + 8 * c : 0;
+      *reinterpret_cast<bf16x8*>(&rope_s[0][8 * idx]) = ok ? *reinterpret_cast<const bf16x8*>(rcs + off) : bf16x8{};
+      *reinterpret_cast<bf16x8*>(&rope_s[1][8 * idx]) = ok ? *reinterpret_cast<const bf16x8*>(rsn + off) : bf16x8{};
+    }
+  }
   // K and V tiles of the workgroup's keys (row-major, swizzled).  K feeds
   // dQ = dS K (transposed reads) and, like V, the per-key MFMA operands of
   // S = Q K^T and dP = dO V^T, which are re-read from LDS every step rather
@@ -943,8 +959,8 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
         }
         if (rcs) {  // RoPE VJP: d = 32db + 8r + 4hl + t, pairs (t, t+1) for t = 0, 2
           const int j0 = (32 * db + 8 * r + 4 * hl) / 2;
-          const bf16x2 c2 = *reinterpret_cast<const bf16x2*>(rcs + (size_t)my_k * (D / 2) + j0);
-          const bf16x2 s2 = *reinterpret_cast<const bf16x2*>(rsn + (size_t)my_k * (D / 2) + j0);
+          const bf16x2 c2 = *reinterpret_cast<const bf16x2*>(&rope_s[0][(32 * wave + l32) * (D / 2) + j0]);
+          const bf16x2 s2 = *reinterpret_cast<const bf16x2*>(&rope_s[1][(32 * wave + l32) * (D / 2) + j0]);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const bf16x2 rr = rope_pair((float)k4[2 * u], (float)k4[2 * u + 1], (float)c2[u], -(float)s2[u]);
