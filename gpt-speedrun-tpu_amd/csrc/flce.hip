@@ -25,12 +25,38 @@ using gemm::BM;
 using gemm::BN;
 using gemm::Operand;
 
+// Column nb of a wave's 128-row accumulator block: scale to the log2 domain in
+// place and return (max, sum exp2(x - max)) over the 128 rows (both lane halves
+// combined).  kMask: rows whose constant part 32mb + 8(i/4) + i%4 is not below
+// lim are padding (-inf); the unmasked copy has no per-element compare.
+template <bool kMask>
+__device__ __forceinline__ float2 column_stats(f32x16 (&acc)[4][2], int nb, int lim) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float y = (!kMask || 32 * mb + 8 * (i >> 2) + (i & 3) < lim) ? acc[mb][nb][i] * GPTRIG_LOG2E : -INFINITY;
+      acc[mb][nb][i] = y;
+      mx = fmaxf(mx, y);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float sum = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sum += fast_exp2(acc[mb][nb][i] - mx);
+  }
+  sum += __shfl_xor(sum, 32);
+  return make_float2(mx, sum);
+}
+
 // ---------------------------------------------------------------------------
 // Forward: partial (max, sum exp) in the log2 domain per token over the tile.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(gemm::THREADS)
-    flce_fwd_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, const int32_t* __restrict__ targets,
-                    float2* __restrict__ partial, float* __restrict__ tlogit) {
+    flce_fwd_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, float2* __restrict__ partial) {
   __shared__ float2 xchg[4][64];
   int tm, tn;
   gemm::tile_coords(blockIdx.x, V, N, tm, tn);
@@ -40,31 +66,13 @@ __global__ void __launch_bounds__(gemm::THREADS)
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
   const int vbase = tm * BM + 128 * wm;
+  const bool full = vbase + 128 <= sem_v;  // no padding row in this wave's 128 rows
+  const int lim = sem_v - vbase - 4 * hl;  // row r of the wave's block is real iff its constant part < lim
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int n = tn * BN + 64 * wn + 32 * nb + l32;
-    const int t = n < N ? targets[n] : -1;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int v = vbase + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
-        const float x = acc[mb][nb][i];
-        if (v == t) tlogit[n] = x;
-        const float y = v < sem_v ? x * GPTRIG_LOG2E : -INFINITY;
-        acc[mb][nb][i] = y;
-        mx = fmaxf(mx, y);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    float sum = 0.f;
-    if (mx != -INFINITY) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sum += fast_exp2(acc[mb][nb][i] - mx);
-    }
-    sum += __shfl_xor(sum, 32);
+    const float2 st = full ? column_stats<false>(acc, nb, lim) : column_stats<true>(acc, nb, lim);
+    const float mx = st.x, sum = st.y;
     if (wm == 1 && hl == 0) xchg[wn][32 * nb + l32] = make_float2(mx, sum);
     __syncthreads();
     if (wm == 0 && hl == 0 && n < N) {
@@ -76,6 +84,68 @@ __global__ void __launch_bounds__(gemm::THREADS)
     }
     __syncthreads();
   }
+}
+
+// Persistent form of the forward for d a multiple of 128 (gemm::persistent):
+// one workgroup per CU walks the tiles, copying the next tile's first stages
+// while this one's epilogue runs.  Same epilogue as flce_fwd_kernel, with
+// LDS-only barriers (a full __syncthreads would wait for those copies).
+__global__ void __launch_bounds__(gemm::THREADS)
+    flce_fwd_persistent_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, float2* __restrict__ partial) {
+  __shared__ float2 xchg[4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int ntiles = ((V + BM - 1) / BM) * ((N + BN - 1) / BN);
+  auto coords = [&](int t, int& tm, int& tn) { gemm::tile_coords(t, V, N, tm, tn); };
+  auto pre = [](int, int) {};
+  auto epi = [&](f32x16(&acc)[4][2], int tm, int tn) {
+    const int vbase = tm * BM + 128 * wm;
+    const bool full = vbase + 128 <= sem_v;
+    const int lim = sem_v - vbase - 4 * hl;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int n = tn * BN + 64 * wn + 32 * nb + l32;
+      const float2 st = full ? column_stats<false>(acc, nb, lim) : column_stats<true>(acc, nb, lim);
+      const float mx = st.x, sum = st.y;
+      if (wm == 1 && hl == 0) xchg[wn][32 * nb + l32] = make_float2(mx, sum);
+      GPTRIG_WAIT_LGKM0();
+      wg_barrier();
+      if (wm == 0 && hl == 0 && n < N) {
+        const float2 o = xchg[wn][32 * nb + l32];
+        const float m2 = fmaxf(mx, o.x);
+        float s2 = 0.f;
+        if (m2 != -INFINITY) s2 = sum * fast_exp2(mx - m2) + o.y * fast_exp2(o.x - m2);
+        partial[(size_t)tm * N + n] = make_float2(m2, s2);
+      }
+      GPTRIG_WAIT_LGKM0();
+      wg_barrier();
+    }
+  };
+  gemm::persistent<true, true>(W, Hd, V, N, D, ntiles, coords, pre, epi);
+}
+
+// Target logit h[n] . W[t[n]] (fp32 accumulation of the bf16 products), 0 for
+// an invalid target: one wave per token.  Taken out of the GEMM epilogue,
+// where a per-element target compare cost more than this pass.
+__global__ void __launch_bounds__(256) flce_target_logit_kernel(const bf16* __restrict__ h, const bf16* __restrict__ w,
+                                                              const int32_t* __restrict__ targets, int N, int D,
+                                                              int sem_v, float* __restrict__ tlogit) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const int t = targets[n];
+  float acc = 0.f;
+  if (t >= 0 && t < sem_v) {
+    for (int c = 8 * lane; c < D; c += 512) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(h + (size_t)n * D + c);
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(w + (size_t)t * D + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf((float)a[j], (float)b[j], acc);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) tlogit[n] = acc;
 }
 
 // lse[n] (natural log) from the per-tile partials; loss = lse - target logit,
@@ -272,8 +342,16 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
   float* tlogit = (float*)((char*)workspace + align256((size_t)ntiles * n * sizeof(float2)));
   hipStream_t s = (hipStream_t)stream;
   Operand W{(const bf16*)weight, d}, Hd{(const bf16*)hidden, d};
-  flce_fwd_kernel<<<tiles_of(vocab, n), gemm::THREADS, 0, s>>>(W, Hd, vocab, n, d, semantic_vocab, targets, partial,
-                                                                tlogit);
+  if (d % (4 * gemm::BK) == 0) {
+    const unsigned tiles = tiles_of(vocab, n), cus = (unsigned)gemm::device_cus();
+    flce_fwd_persistent_kernel<<<tiles < cus ? tiles : cus, gemm::THREADS, 0, s>>>(W, Hd, vocab, n, d, semantic_vocab,
+                                                                                   partial);
+  } else {
+    flce_fwd_kernel<<<tiles_of(vocab, n), gemm::THREADS, 0, s>>>(W, Hd, vocab, n, d, semantic_vocab, partial);
+  }
+  GPTRIG_CHECK_LAUNCH();
+  flce_target_logit_kernel<<<ceil_div(n, 4), 256, 0, s>>>((const bf16*)hidden, (const bf16*)weight, targets, n, d,
+                                                           semantic_vocab, tlogit);
   GPTRIG_CHECK_LAUNCH();
   flce_combine_kernel<<<ceil_div(n, 256), 256, 0, s>>>(partial, ntiles, n, semantic_vocab, targets, tlogit, lse,
                                                         losses);

@@ -255,6 +255,88 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand
   GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
 }
 
+// One stage of the persistent form: as step(), but the refill of buffer S
+// comes from `fc` at stage fkt (the next tile's sources once the current tile
+// has no stages left to copy).
+template <bool AK, bool BKM, int S, bool kReadNext = true>
+__device__ __forceinline__ void step_fill(f32x16 (&acc)[4][2], const Ctx& c, const Ctx& fc, int fkt, bf16x8 (&a0)[4],
+                                          bf16x8 (&b0)[2]) {
+  bf16x8 a1[4], b1[2];
+  read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
+  mma_half(acc, a0, b0);
+  GEMM_WAIT_VM8_LGKM0();
+  wg_barrier();
+  fill(stage_ptr<S>(), fc, fkt);
+  if (kReadNext) read_half<AK, BKM>(a0, b0, stage_ptr<(S + 1) % 4>(), 0, c);
+  mma_half(acc, a1, b1);
+}
+
+// Persistent form of mainloop for K a multiple of 4*BK (every tile then
+// starts at stage buffer 0): the workgroup runs tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ... over the full K range, and the first four
+// stages of its next tile are copied during the last four stages of the
+// current one, so the epilogue runs while the next operands are in flight.
+// coords(t, tm, tn) maps a tile index to tile coordinates; pre(tm, tn) runs
+// before each tile's stages (after the previous tile's epilogue), e.g. to
+// prefetch per-tile epilogue inputs far ahead of their use; epi(acc, tm, tn)
+// must not touch the stage arrays (its own LDS and barriers are fine).
+template <bool AK, bool BKM, class Coords, class Pre, class Epi>
+__device__ __forceinline__ void persistent(Operand A, Operand B, int M, int N, int K, int ntiles, Coords coords,
+                                           Pre pre, Epi epi) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform
+  const int nk = K / BK;
+  int tm, tn;
+  coords(t, tm, tn);
+  Ctx c{make_src<AK>(A, tm * BM, 0, M, K, wave, lane), make_src<BKM>(B, tn * BN, 0, N, K, wave, lane),
+        128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid};
+  fill(stage_ptr<0>(), c, 0);
+  fill(stage_ptr<1>(), c, 1);
+  fill(stage_ptr<2>(), c, 2);
+  fill(stage_ptr<3>(), c, 3);
+  pre(tm, tn);
+  GEMM_WAIT_VM12_LGKM0();
+  wg_barrier();
+  bf16x8 a0[4], b0[2];
+  read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
+  f32x16 acc[4][2];
+  while (true) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
+    for (int kt = 0; kt < nk - 4; kt += 4) {
+      step_fill<AK, BKM, 0>(acc, c, c, kt + 4, a0, b0);
+      step_fill<AK, BKM, 1>(acc, c, c, kt + 5, a0, b0);
+      step_fill<AK, BKM, 2>(acc, c, c, kt + 6, a0, b0);
+      step_fill<AK, BKM, 3>(acc, c, c, kt + 7, a0, b0);
+    }
+    const int t_next = t + (int)gridDim.x;
+    const bool has_next = t_next < ntiles;
+    int tm_n = 0, tn_n = 0;
+    if (has_next) coords(t_next, tm_n, tn_n);
+    // Sources of the next tile; with none, extents of 0 make every copy read zeros.
+    const Ctx cn{make_src<AK>(A, tm_n * BM, 0, has_next ? M : 0, K, wave, lane),
+                 make_src<BKM>(B, tn_n * BN, 0, has_next ? N : 0, K, wave, lane), c.wm0, c.wn0, wave, lane, tid};
+    step_fill<AK, BKM, 0>(acc, c, cn, 0, a0, b0);
+    step_fill<AK, BKM, 1>(acc, c, cn, 1, a0, b0);
+    step_fill<AK, BKM, 2>(acc, c, cn, 2, a0, b0);
+    // (The next tile's first fragments are read after the epilogue, so they
+    // are not live across it.)
+    step_fill<AK, BKM, 3, false>(acc, c, cn, 3, a0, b0);
+    epi(acc, tm, tn);
+    if (!has_next) break;
+    pre(tm_n, tn_n);
+    t = t_next;
+    tm = tm_n;
+    tn = tn_n;
+    c = cn;
+    read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
+  }
+  GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // Give XCD x a contiguous range of logical tile ids so that the tiles sharing
 // A/B slabs run on the same L2.
