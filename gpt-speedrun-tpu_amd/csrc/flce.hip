@@ -233,6 +233,79 @@ __global__ void __launch_bounds__(gemm::THREADS)
   }
 }
 
+// Persistent form of K1 for d a multiple of 128 (gemm::persistent), computing
+// the transposed product: m = token, n = vocabulary row, so each lane holds
+// four consecutive tokens of one vocabulary row and writes them to G^T as one
+// 8-byte store straight from registers (the stage arrays stay free for the
+// next tile's copies).  Per-token lse / cotangent / target are staged in LDS,
+// double-buffered by tile parity and loaded a tile ahead.  Tiles are walked
+// in the order of flce_grad_kernel (two vocabulary tiles per token sweep).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(gemm::THREADS)
+    flce_grad_persistent_kernel(Operand W, Operand Hd, int Vc, int N, int D, int v0, int sem_v,
+                                const int32_t* __restrict__ targets, const float* __restrict__ lse,
+                                const float* __restrict__ cot, float cot_scale, bf16* __restrict__ gt) {
+  __shared__ __attribute__((aligned(16))) float l2_s[2][BM];
+  __shared__ __attribute__((aligned(16))) float ct_s[2][BM];
+  __shared__ __attribute__((aligned(16))) int t_s[2][BM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int ntiles = ((Vc + BM - 1) / BM) * ((N + BN - 1) / BN);
+  int pre_it = 0, epi_it = 0;
+  auto coords = [&](int t, int& tm, int& tn) {
+    int tv, tt;
+    gemm::tile_coords(t, Vc, N, tv, tt, 2);
+    tm = tt;  // token tile
+    tn = tv;  // vocabulary tile
+  };
+  auto pre = [&](int tm, int) {
+    const int b = pre_it & 1;
+    ++pre_it;
+    if (tid < BM) {
+      const int n = tm * BM + tid;
+      const bool n_ok = n < N;
+      const int t = n_ok ? targets[n] : -1;
+      const bool valid_t = t >= 0 && t < sem_v;
+      t_s[b][tid] = t;
+      ct_s[b][tid] = valid_t ? (cot ? cot[n] : cot_scale) : 0.f;
+      l2_s[b][tid] = n_ok ? lse[n] * GPTRIG_LOG2E : 0.f;
+    }
+  };
+  auto epi = [&](f32x16(&acc)[4][2], int tm, int tn) {
+    const int b = epi_it & 1;
+    ++epi_it;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r0 = 128 * wm + 32 * mb + 8 * q + 4 * hl;  // 4 consecutive tokens of the tile
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&l2_s[b][r0]);
+        const f32x4 c4 = *reinterpret_cast<const f32x4*>(&ct_s[b][r0]);
+        const i32x4_t t4 = *reinterpret_cast<const i32x4_t*>(&t_s[b][r0]);
+        const int n = tm * BM + r0;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int vl = tn * BN + 64 * wn + 32 * nb + l32;
+          const int v = v0 + vl;
+          bf16x4 o;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float g = 0.f;
+            if (v < sem_v) {
+              const float p = fast_exp2(acc[mb][nb][4 * q + j] * GPTRIG_LOG2E - l4[j]);
+              g = (p - (v == t4[j] ? 1.f : 0.f)) * c4[j];
+            }
+            o[j] = (bf16)g;
+          }
+          // N is a multiple of 8 and n of 4, so n < N covers n .. n+3.
+          if (vl < Vc && n < N) *reinterpret_cast<bf16x4*>(gt + (size_t)vl * N + n) = o;
+        }
+      }
+  };
+  gemm::persistent<true, true>(Hd, W, N, Vc, D, ntiles, coords, pre, epi);
+}
+
 // C (fp32, row-major [M][ldc]) = / += / atomic+= A B over K range of this split.
 // mode 0: store, 1: accumulate (read-modify-write), 2: atomic add.
 // colsum (nullable): colsum[n] atomic+= sum over this split's
@@ -395,8 +468,14 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
   for (int v0 = 0; v0 < vocab; v0 += chunk) {
     const int vc = vocab - v0 < chunk ? vocab - v0 : chunk;
     Operand Wc{Wp + (size_t)v0 * d, d}, Hd{Hp, d};
-    flce_grad_kernel<<<tiles_of(vc, n), gemm::THREADS, 0, s>>>(Wc, Hd, vc, n, d, v0, semantic_vocab, targets, lse,
-                                                                cotangent, cotangent_scale, gt);
+    if (d % (4 * gemm::BK) == 0) {
+      const unsigned tiles = tiles_of(vc, n), cus = (unsigned)gemm::device_cus();
+      flce_grad_persistent_kernel<<<tiles < cus ? tiles : cus, gemm::THREADS, 0, s>>>(
+          Wc, Hd, vc, n, d, v0, semantic_vocab, targets, lse, cotangent, cotangent_scale, gt);
+    } else {
+      flce_grad_kernel<<<tiles_of(vc, n), gemm::THREADS, 0, s>>>(Wc, Hd, vc, n, d, v0, semantic_vocab, targets, lse,
+                                                                  cotangent, cotangent_scale, gt);
+    }
     GPTRIG_CHECK_LAUNCH();
     // dW[v0:v0+vc] += G^T h : A = G^T [vc][n] (K-major), B = h [n][d] (MN-major); split over tokens.
     Operand Ag{gt, n}, Bh{Hp, d};
