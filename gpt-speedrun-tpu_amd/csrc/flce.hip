@@ -11,7 +11,8 @@
 //   backward (:220-302)  per vocabulary chunk (bounded workspace, like the
 //            reference's [n, tile] live logits):
 //            K1  recompute logits^T, write G^T = bf16((exp(logit-lse) - onehot)*ct)
-//                as [chunk, n] (zero for rows >= semantic vocab);
+//                as [chunk, n] in 32-token column blocks (gemm::Operand blk),
+//                zero for rows >= semantic vocab;
 //            K2  dW[chunk] += G^T h     (split over tokens, fp32 atomics);
 //            K3  dh_acc    += G W[chunk] (fp32 atomics, split over the chunk),
 //                rounded to bf16 at the end.
@@ -228,7 +229,8 @@ __global__ void __launch_bounds__(gemm::THREADS)
     // in L2.
     if (vl < Vc && n < N) {
       const bf16x8 g8 = *(const gemm::lds_x8*)(band[r >> 6] + (r & 63) * 256 + 8 * c);
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, g8), reinterpret_cast<u32x4*>(gt + (size_t)vl * N + n));
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, g8),
+                                  reinterpret_cast<u32x4*>(gt + ((size_t)(n >> 5) * Vc + vl) * 32 + (n & 31)));
     }
   }
 }
@@ -299,7 +301,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
             o[j] = (bf16)g;
           }
           // N is a multiple of 8 and n of 4, so n < N covers n .. n+3.
-          if (vl < Vc && n < N) *reinterpret_cast<bf16x4*>(gt + (size_t)vl * N + n) = o;
+          if (vl < Vc && n < N) *reinterpret_cast<bf16x4*>(gt + ((size_t)(n >> 5) * Vc + vl) * 32 + (n & 31)) = o;
         }
       }
   };
@@ -434,7 +436,7 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
 
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk) {
   const int chunk = resolve_chunk(vocab, vocab_chunk);
-  return align256((size_t)chunk * n * sizeof(bf16)) + align256((size_t)n * d * sizeof(float));
+  return align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16)) + align256((size_t)n * d * sizeof(float));
 }
 
 int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
@@ -451,7 +453,7 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     return GPTRIG_E_SHAPE;
   const int chunk = resolve_chunk(vocab, vocab_chunk);
   bf16* gt = (bf16*)workspace;
-  float* dh_acc = (float*)((char*)workspace + align256((size_t)chunk * n * sizeof(bf16)));
+  float* dh_acc = (float*)((char*)workspace + align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16)));
   hipStream_t s = (hipStream_t)stream;
   const bf16* Wp = (const bf16*)weight;
   const bf16* Hp = (const bf16*)hidden;
@@ -478,13 +480,13 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     }
     GPTRIG_CHECK_LAUNCH();
     // dW[v0:v0+vc] += G^T h : A = G^T [vc][n] (K-major), B = h [n][d] (MN-major); split over tokens.
-    Operand Ag{gt, n}, Bh{Hp, d};
+    Operand Ag{gt, n, vc}, Bh{Hp, d};
     const int dw_split = gemm::choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
     gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(
         Ag, Bh, vc, d, n, dw_split, dweight + (size_t)v0 * d, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
     // dh += G W[v0:v0+vc] : A(m=n, k=v) = G^T [vc][n] (MN-major), B(k=v, n=j) = W [vc][d] (MN-major).
-    Operand Agt{gt, n}, Bw{Wp + (size_t)v0 * d, d};
+    Operand Agt{gt, n, vc}, Bw{Wp + (size_t)v0 * d, d};
     const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
     gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
                                                                                         dh_acc, d, 2, nullptr);

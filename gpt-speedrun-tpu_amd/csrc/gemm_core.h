@@ -62,9 +62,15 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void gbl_void;
 typedef const __attribute__((address_space(1))) bf16x8 gbl_x8;
 
+// A matrix operand: row-major with leading dimension ld, or (blk > 0)
+// "32-blocked": element (r, c) at ((c / 32) * blk + r) * 32 + c % 32, i.e.
+// column blocks of 32 stored one after another, each as blk rows of 64 bytes
+// (so a 32-deep K-major stage, or the rows of an MN-major stage, read whole
+// contiguous runs instead of 64-byte pieces of longer rows).
 struct Operand {
   const bf16* p;
   int64_t ld;
+  int64_t blk = 0;
 };
 
 __device__ __forceinline__ lds_t* lds_cast(bf16* p) { return (lds_t*)p; }
@@ -102,19 +108,24 @@ __device__ __forceinline__ Src make_src(Operand op, int mn0, int k_begin, int MN
       const int row = blk * 16 + (lane >> 2);
       const int c = (lane & 3) ^ ((row >> 2) & 3);
       const int m = mn0 + row;
-      s.base[j] = op.p + (int64_t)(m < MN ? m : 0) * op.ld + k_begin + 8 * c;
+      const int64_t mm = m < MN ? m : 0;
+      // (k_begin is a multiple of BK = 32, so blocked stages start on a block.)
+      s.base[j] = op.blk ? op.p + ((int64_t)(k_begin >> 5) * op.blk + mm) * 32 + 8 * c
+                         : op.p + mm * op.ld + k_begin + 8 * c;
       const int rem = k_end - k_begin - 8 * c;
       s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
     } else {
       const int row = blk * 2 + (lane >> 5);
       const int c = (lane & 31) ^ (4 * (row & 3));
       const int m = mn0 + 8 * c;
-      s.base[j] = op.p + (int64_t)(k_begin + row) * op.ld + (m < MN ? m : 0);
+      const int64_t mm = m < MN ? m : 0;
+      s.base[j] = op.blk ? op.p + ((mm >> 5) * op.blk + k_begin + row) * 32 + (mm & 31)
+                         : op.p + (int64_t)(k_begin + row) * op.ld + mm;
       const int rem = k_end - k_begin - row;
       s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
     }
   }
-  s.step = KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld;
+  s.step = op.blk ? (KMAJOR ? op.blk * 32 : (int64_t)BK * 32) : (KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld);
   return s;
 }
 
