@@ -542,22 +542,31 @@ __global__ void rope_view_bwd_kernel(MutView X, int B, int H, int S, int D, cons
 // ============================================================================
 // head_dim 64 kernels on swizzled row-major LDS tiles (attn64.h)
 // ============================================================================
-__device__ const bf16x8 kZeroChunk[2] = {};
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef const __attribute__((address_space(1))) void gbl_void;
 
 // Forward: K/V tiles of 64 keys are copied global -> LDS by the DMA path
-// (global_load_lds_dwordx4) into double-buffered swizzled tiles; V^T operands
-// come from transposed reads with the accumulator's row order.
+// (buffer_load_dwordx4 ... lds) into double-buffered swizzled tiles, one LDS array
+// per buffer and operand so the compiler can see that the copy into one
+// buffer never aliases reads of the other; V^T operands come from transposed
+// reads with the accumulator's row order.  A tile is consumed in two halves
+// of 32 keys (online softmax per half), which keeps the wave under 128 VGPRs:
+// four waves per SIMD hide the LDS and exp latencies.
+__shared__ __attribute__((aligned(16))) bf16 g_fk0[64 * 64];
+__shared__ __attribute__((aligned(16))) bf16 g_fk1[64 * 64];
+__shared__ __attribute__((aligned(16))) bf16 g_fv0[64 * 64];
+__shared__ __attribute__((aligned(16))) bf16 g_fv1[64 * 64];
+
+template <int BUF>
+__device__ __forceinline__ at64::lds_t* fwd_k() { return gemm::lds_cast(BUF ? g_fk1 : g_fk0); }
+template <int BUF>
+__device__ __forceinline__ at64::lds_t* fwd_v() { return gemm::lds_cast(BUF ? g_fv1 : g_fv0); }
+
 template <bool kSeg>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, 4)
     attn_fwd64_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
                       int B, int H, int S, float scale_log2) {
-  constexpr int D = 64, KC = 4, DB = 2, TILE = 64 * 64;
-  __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K[2], V[2]
-  at64::lds_t* const Kt = gemm::lds_cast(smem);
-  at64::lds_t* const Vt = Kt + 2 * TILE;
+  constexpr int D = 64, KC = 4, DB = 2;
 
   const int nq = (S + kBlockM - 1) / kBlockM;
   int bh, qb;
@@ -583,108 +592,101 @@ __global__ void __launch_bounds__(256, 2)
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
   float m_run = kMinusBig, l_run = 0.f;
 
-  // Wave w fills 1 KB blocks 2w, 2w+1 (8 rows each) of the K and V tiles.
-  auto fill = [&](int buf, int kv0) {
+  // Wave w fills 1 KB blocks 2w, 2w+1 (8 rows each) of the K and V tiles
+  // through buffer resources of this (b, h): 32-bit per-lane offsets, and
+  // rows at or past S read as zeros.
+  const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(K.row(b, h, 0), (uint32_t)(S * K.ss * 2));
+  const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(V.row(b, h, 0), (uint32_t)(S * V.ss * 2));
+  const int kss2 = (int)K.ss * 2, vss2 = (int)V.ss * 2;
+  int koff[2], voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = 8 * (2 * wave + j) + (lane >> 3);
+    const int t = (row >> 1) & 7;
+    const int c = (lane & 7) ^ (((t & 1) << 2) | (t >> 1));
+    koff[j] = row * kss2 + 16 * c;
+    voff[j] = row * vss2 + 16 * c;
+  }
+  auto fill = [&](at64::lds_t* kt, at64::lds_t* vt, int kv0) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int blk = 2 * wave + j;
-      const int row = 8 * blk + (lane >> 3);
-      const int t = (row >> 1) & 7;
-      const int c = (lane & 7) ^ (((t & 1) << 2) | (t >> 1));
-      const bool ok = kv0 + row < S;
-      const bf16* ks = ok ? K.row(b, h, kv0 + row) + 8 * c : (const bf16*)kZeroChunk;
-      const bf16* vs = ok ? V.row(b, h, kv0 + row) + 8 * c : (const bf16*)kZeroChunk;
-      __builtin_amdgcn_global_load_lds((gbl_void*)ks, (lds_void*)(Kt + buf * TILE + blk * 512), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((gbl_void*)vs, (lds_void*)(Vt + buf * TILE + blk * 512), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, (lds_void*)(kt + blk * 512), 16, koff[j] + kv0 * kss2, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rs, (lds_void*)(vt + blk * 512), 16, voff[j] + kv0 * vss2, 0, 0, 0);
     }
   };
 
-  fill(0, 0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int kv0 = it * kBlockN;
-    const at64::lds_t* kt = Kt + buf * TILE;
-    const at64::lds_t* vt = Vt + buf * TILE;
-    const bool active = kv0 <= qw0 + 31;  // some key of this tile is visible to this wave
-    // All reads of this tile are issued before the prefetch into the other
-    // buffer, so no LDS-DMA ordering wait separates them.
-    bf16x8 kf[2][KC], vf[DB][4];
-    if (active) {
+  // One 32-key half of a tile in buffer (kt, vt).
+  auto half = [&](const at64::lds_t* kt, const at64::lds_t* vt, int kv0, int sb) {
+    f32x16 s = f32x16{};
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+    for (int kc = 0; kc < KC; ++kc) s = mfma32(at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl), qreg[kc], s);
+    // Row max on raw scores (scale > 0); masked scores become -inf.
+    const int kh0 = kv0 + 32 * sb;
+    const bool need_mask = (kh0 + 31 > qw0) || (kh0 + 32 > S) || kSeg;
+    float mraw = -INFINITY;
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) kf[sb][kc] = at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl);
+    for (int i = 0; i < 16; ++i) {
+      if (need_mask) {
+        const int key = kh0 + 8 * (i >> 2) + 4 * hl + (i & 3);
+        bool vis = key <= my_q && key < S;
+        if (kSeg && vis) vis = seg[(size_t)b * S + key] == seg_q;
+        s[i] = vis ? s[i] : -INFINITY;
+      }
+      mraw = fmaxf(mraw, s[i]);
+    }
+    mraw = fmaxf(mraw, __shfl_xor(mraw, 32));
+    // Lazy rescaling: the running max (log2 units) only moves when a row's
+    // max exceeds it by more than 8, so probabilities stay <= 2^8 and the
+    // accumulator rescale is skipped on most halves.  O = acc / l and
+    // lse = m + log2(l) hold for any consistent m.
+    const float m_tile = mraw * scale_log2;
+    const bool grow = m_tile > m_run + 8.0f;
+    const float m_new = grow ? m_tile : m_run;
+    if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) vf[db][c] = at64::trfrag<true>(vt, 32 * db, 16 * c, lane);
+        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
     }
-    if (it + 1 < ntiles) fill(buf ^ 1, kv0 + kBlockN);
+    m_run = m_new;
+    float lsum = 0.f;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = fast_exp2(fmaf(s[8 * c2 + j], scale_log2, -m_new));
+        lsum += p;
+        pb[c2][j] = (bf16)p;
+      }
+    l_run += lsum;
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        acc[db] = mfma32(at64::trfrag<true>(vt, 32 * db, 16 * (2 * sb + c2), lane), pb[c2], acc[db]);
+  };
 
-    if (active) {
-      f32x16 s[2];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        s[sb] = f32x16{};
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) s[sb] = mfma32(kf[sb][kc], qreg[kc], s[sb]);
-      }
-      // Row max on raw scores (scale > 0); masked scores become -inf.
-      const bool need_mask = (kv0 + kBlockN - 1 > qw0) || (kv0 + kBlockN > S) || kSeg;
-      float mraw = -INFINITY;
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (need_mask) {
-            const int key = kv0 + 32 * sb + 8 * (i >> 2) + 4 * hl + (i & 3);
-            bool vis = key <= my_q && key < S;
-            if (kSeg && vis) vis = seg[(size_t)b * S + key] == seg_q;
-            s[sb][i] = vis ? s[sb][i] : -INFINITY;
-          }
-          mraw = fmaxf(mraw, s[sb][i]);
-        }
-      }
-      mraw = fmaxf(mraw, __shfl_xor(mraw, 32));
-      // Lazy rescaling: the running max (log2 units) only moves when a row's
-      // max exceeds it by more than 8, so probabilities stay <= 2^8 and the
-      // accumulator rescale is skipped on most tiles.  O = acc / l and
-      // lse = m + log2(l) hold for any consistent m.
-      const float m_tile = mraw * scale_log2;
-      const bool grow = m_tile > m_run + 8.0f;
-      const float m_new = grow ? m_tile : m_run;
-      if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
-        const float alpha = fast_exp2(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-      }
-      m_run = m_new;
-      float lsum = 0.f;
-      bf16x8 pb[4];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float p = fast_exp2(fmaf(s[sb][8 * c2 + j], scale_log2, -m_new));
-            lsum += p;
-            pb[2 * sb + c2][j] = (bf16)p;
-          }
-      l_run += lsum;
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] = mfma32(vf[db][c], pb[c], acc[db]);
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+  auto tile = [&](const at64::lds_t* kt, const at64::lds_t* vt, at64::lds_t* nkt, at64::lds_t* nvt, int it) {
+    const int kv0 = it * kBlockN;
+    if (it + 1 < ntiles) fill(nkt, nvt, kv0 + kBlockN);
+    // Halves whose every key lies past the wave's last query add nothing.
+    if (kv0 <= qw0 + 31) half(kt, vt, kv0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the halves' live ranges apart
+    if (kv0 + 32 <= qw0 + 31) half(kt, vt, kv0, 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
     __syncthreads();
+  };
+
+  fill(fwd_k<0>(), fwd_v<0>(), 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  for (int it = 0; it < ntiles; it += 2) {
+    tile(fwd_k<0>(), fwd_v<0>(), fwd_k<1>(), fwd_v<1>(), it);
+    if (it + 1 < ntiles) tile(fwd_k<1>(), fwd_v<1>(), fwd_k<0>(), fwd_v<0>(), it + 1);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -1016,6 +1018,8 @@ int gptrig_attn_fwd(const void* q, const void* k, const void* v, const int32_t* 
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 64)
   {
+    // The kernel copies one (b, h) slice of K / V through 32-bit buffer offsets.
+    if ((long long)seq * (K.ss > V.ss ? K.ss : V.ss) * 2 >= (1ll << 31)) return GPTRIG_E_SHAPE;
     if (segment_ids)
       attn_fwd64_kernel<true><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
     else
