@@ -39,7 +39,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # launches, from `rocprofv3 --pmc` runs of this tree; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes.
-FLCE_TRAFFIC_BYTES = (21120 + 4801) * 2 ** 20
+FLCE_TRAFFIC_BYTES = (17909 + 5159) * 2 ** 20
 
 
 def parse_args():
