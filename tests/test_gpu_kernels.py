@@ -140,6 +140,7 @@ def test_attention_full_config_b_slice_matches_oracle():
 FLCE_CASES = [
     # (n, d, V, semantic V, chunk)
     (296, 128, 1000, 997, 256),
+    (200, 64, 700, 650, 512),       # d not a multiple of 128: the non-persistent launches
     (256, 768, 259, 257, 256),      # reference wide-target test shape (tests/test_linear_cross_entropy.py:154-187)
     (512, 768, 50304, 50257, 4096),
 ]
