@@ -3,7 +3,7 @@
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
 
 Workload: 12 layers, d_model 768, 12 heads x 64, GELU MLP 3072, vocab 50304,
-seq 1024, global batch 128 sequences as 4 micro-batches of 32, AdamW
+seq 1024, global batch 128 sequences (by default as 2 micro-batches of 64), AdamW
 (base LR 2^-8, betas 0.9/0.95, wd 0.1), bf16 compute with float32 master
 weights, synthetic uniform tokens from numpy seed 2, random-normal init
 (std 0.02) — the full step (forward, backward, AdamW) every iteration.
@@ -33,13 +33,13 @@ import torch  # noqa: E402
 
 METRIC = "train tokens/s at 125M S=1024; attn-bwd + FLCE TFLOP/s as % of bf16 MFMA peak"
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-# HBM bytes of one FLCE fwd+bwd launch sequence at the bench shape (N 32768,
-# d 768, V 50304, three vocabulary chunks): FETCH_SIZE (x 2.0, the factor the
-# counter reads for a 256 MiB copy) + WRITE_SIZE (x 1.0) summed over its
-# launches, from `rocprofv3 --pmc` runs of this tree; the per-launch table and
+# HBM bytes of one FLCE fwd+bwd launch sequence, by micro-batch tokens N (d 768,
+# V 50304, three vocabulary chunks): FETCH_SIZE (x 2.0, the factor the counter
+# reads for a 256 MiB copy) + WRITE_SIZE (x 1.0) summed over its launches, from
+# `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes.
-FLCE_TRAFFIC_BYTES = (17909 + 5159) * 2 ** 20
+FLCE_TRAFFIC_BYTES = {32768: (17909 + 5159) * 2 ** 20, 65536: (35131 + 8632) * 2 ** 20}
 
 
 def parse_args():
@@ -47,18 +47,20 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--micro-batch", type=int, default=32)
+    ap.add_argument("--micro-batch", type=int, default=64,
+                    help="sequences per forward/backward pass (the global batch of 128 is accumulated over 128 / micro-batch passes; 64 measured fastest: at 128 the attention working set outgrows the L2 + MALL)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="approximate CPU-baseline budget")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="run one 256 MiB calibration copy, one FLCE forward+backward and one attention "
-                         "forward+backward at the bench shapes, and exit (the program profiled by the "
-                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
+                         "forward+backward at the bench's micro-batch shapes, and exit (the program profiled by "
+                         "the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     return ap.parse_args()
 
 
-def traffic_pass() -> None:
-    """One launch sequence of each hand-written hot path, for HBM-counter runs."""
+def traffic_pass(micro_batch: int) -> None:
+    """One launch sequence of each hand-written hot path at the bench's
+    micro-batch shape, for HBM-counter runs."""
 
     from gptrig.kernels import flash_attention as fa
     from gptrig.kernels import linear_cross_entropy as lce
@@ -68,14 +70,14 @@ def traffic_pass() -> None:
     src = torch.randn(64 * 1024 * 1024, device=dev)  # 256 MiB: calibrates the counters
     torch.empty_like(src).copy_(src)
     torch.cuda.synchronize()
-    n, d, vocab = 32768, 768, 50304
+    n, d, vocab = micro_batch * 1024, 768, 50304
     h = torch.randn(n, d, device=dev).bfloat16()
     w = (torch.randn(vocab, d, device=dev) * 0.02).bfloat16()
     t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32)
     _, lse = lce.flce_forward(h, w, t, vocab)
     lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.chunk_for(-(-vocab // 3)))
     torch.cuda.synchronize()
-    q, k, v, do = (torch.randn(32, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
+    q, k, v, do = (torch.randn(micro_batch, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
     o, lse2 = fa.flash_forward(q, k, v, None, 0.125)
     fa.flash_backward(q, k, v, o, lse2, do, None, 0.125)
     torch.cuda.synchronize()
@@ -145,7 +147,7 @@ def cpu_baseline(seconds: float) -> dict:
 def main():
     args = parse_args()
     if args.traffic_pass:
-        traffic_pass()
+        traffic_pass(args.micro_batch)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU (--gpus > 1) is not implemented",
@@ -191,6 +193,7 @@ def main():
 
     n_micro = cfg.batch_size // cfg.micro_batch_size
     mb_tokens = cfg.micro_batch_size * cfg.seq_len
+    traffic = FLCE_TRAFFIC_BYTES.get(mb_tokens)  # measured per shape; None for an unmeasured one
     # FLCE: one forward + one backward launch per micro-batch; report per micro-batch (fwd+bwd).
     flce_ms_launch, flce_n = avg_ms("flce")
     flce_ms = 2 * flce_ms_launch
@@ -217,16 +220,18 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "config D: reference GPT 125M (12x768, 12 heads x 64, mlp 3072, vocab 50304) "
-                               "full train step, S=1024, global batch 128 as 4 micro-batches of 32, AdamW",
+                               f"full train step, S=1024, global batch 128 as {n_micro} micro-batches of "
+                               f"{cfg.micro_batch_size}, AdamW",
                    "global_batch": cfg.batch_size, "micro_batch": cfg.micro_batch_size, "seq_len": cfg.seq_len,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "flce (fused LM-head cross-entropy fwd+bwd, per 32x1024-token micro-batch)",
+        "roofline": {"kernel": f"flce (fused LM-head cross-entropy fwd+bwd, per {cfg.micro_batch_size}x1024-token "
+                               "micro-batch)",
                      "bound": "mfma", "achieved": round(flce_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flce_tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": FLCE_TRAFFIC_BYTES, "traffic_GBps": round(FLCE_TRAFFIC_BYTES / flce_ms / 1e6, 1),
+                     "traffic": traffic, "traffic_GBps": None if traffic is None else round(traffic / flce_ms / 1e6, 1),
                      "ms": round(flce_ms, 3), "algorithmic_flops": flce_flops(mb_tokens, cfg.d_model,
                                                                               cfg.vocab_size)},
-        "roofline_attn_bwd": {"kernel": "attn_bwd (B32 H12 S1024 D64 causal)", "bound": "mfma",
+        "roofline_attn_bwd": {"kernel": f"attn_bwd (B{cfg.micro_batch_size} H12 S1024 D64 causal)", "bound": "mfma",
                               "achieved": round(ab_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(ab_tf / MFMA_BF16_PEAK_TFLOPS, 4), "ms": round(ab_ms, 3)},
         "step_tflops": round(total_flops / (ms_per_step / 1e3) / 1e12, 1),
