@@ -5,14 +5,15 @@
 //
 //   forward  (:115-179)  C = logits^T tile = W_tile h^T (m = vocabulary row,
 //            n = token) -> per-token partial (max, sum exp) over the tile's
-//            256 vocabulary rows + the target logit; a combine pass gives
+//            256 vocabulary rows (persistent launch when d % 128 == 0); the
+//            target logit h . W[t] in its own pass; a combine pass gives
 //            lse and loss = lse - target_logit.  The [n, vocab] logits never
 //            exist.
 //   backward (:220-302)  per vocabulary chunk (bounded workspace, like the
 //            reference's [n, tile] live logits):
-//            K1  recompute logits^T, write G^T = bf16((exp(logit-lse) - onehot)*ct)
+//            K1  recompute the logits, write G^T = bf16((exp(logit-lse) - onehot)*ct)
 //                as [chunk, n] in 32-token column blocks (gemm::Operand blk),
-//                zero for rows >= semantic vocab;
+//                zero for rows >= semantic vocab (persistent when d % 128 == 0);
 //            K2  dW[chunk] += G^T h     (split over tokens, fp32 atomics);
 //            K3  dh_acc    += G W[chunk] (fp32 atomics, split over the chunk),
 //                rounded to bf16 at the end.
