@@ -330,8 +330,8 @@ __global__ void __launch_bounds__(gemm::THREADS)
   // Every M tile of a (tn, split) sums a share of the B stages, so the
   // column sums cost each workgroup the same.
   const bool do_colsum = colsum != nullptr;
-  gemm::mainloop<AK, BKM, true>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, csum,
-                                do_colsum ? (M + BM - 1) / BM : 0, tm);
+  gemm::mainloop_pp<AK, BKM, true>(acc, A, B, M, N, k_begin, k_end, tm * BM, tn * BN, csum,
+                                   do_colsum ? (M + BM - 1) / BM : 0, tm);
   if (k_begin >= k_end) return;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;

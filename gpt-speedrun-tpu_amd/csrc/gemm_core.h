@@ -4,8 +4,9 @@
 // each wave owning a 128 x 64 sub-tile as 4 x 2 blocks of
 // v_mfma_f32_32x32x16_bf16.  K advances in stages of 32.
 //
-// Operand staging: global_load_lds_dwordx4 copies each 16-byte chunk straight
-// from global memory into LDS (no registers, no LDS store instructions),
+// Operand staging: buffer_load_dwordx4 ... lds copies each 16-byte chunk
+// straight from global memory into LDS (no registers, no LDS store
+// instructions),
 // through a 4-stage ring of separate LDS arrays (4 x 32 KB).  Stage kt is
 // waited for with an exact vmcnt (the loads of the two younger stages stay in
 // flight) followed by a bare s_barrier -- __syncthreads() would drain every
@@ -49,7 +50,6 @@ __shared__ __attribute__((aligned(1024))) bf16 g_stage0[STE];
 __shared__ __attribute__((aligned(1024))) bf16 g_stage1[STE];
 __shared__ __attribute__((aligned(1024))) bf16 g_stage2[STE];
 __shared__ __attribute__((aligned(1024))) bf16 g_stage3[STE];
-__device__ const bf16x8 g_zero_chunk[4] = {};
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 // Address-space-qualified views: LDS (3) so fragment traffic is ds_read/ds_write,
@@ -89,18 +89,36 @@ __device__ __forceinline__ lds_t* stage_ptr() {
 }
 
 // Per-lane copy sources of one operand: the wave fills 1 KB blocks 2w and
-// 2w+1 of each 16 KB slab.  base[j] is the global address at stage 0, step
-// the per-stage stride, nvalid[j] the number of stages whose 16 bytes lie in
-// [k_begin, k_end) and inside the M/N extent (later stages read zeros).
+// 2w+1 of each 16 KB slab with buffer_load_dwordx4 ... lds.  base is the
+// operand's address at the tile origin and k_begin, step the bytes per stage
+// (both uniform, so a stage's buffer resource is built in scalar registers);
+// off[j] is the lane's byte offset from base, nvalid[j] the number of stages
+// whose 16 bytes lie in [k_begin, k_end) and inside the M/N extent.  Later
+// stages use an offset past the resource's range, which reads zeros.
+// (The buffer form, unlike global_load_lds, is not taken by the compiler as
+// a possible LDS access in flight, so its fragment reads keep exact lgkmcnt
+// waits instead of lgkmcnt(0) while copies are outstanding.)
 struct Src {
-  const bf16* base[2];
+  const char* base;
   int64_t step;
+  uint32_t off[2];
   int nvalid[2];
 };
+
+constexpr uint32_t kRsrcRange = 0x7FFFFFFFu;  // bytes a stage's resource covers
+constexpr uint32_t kOffZero = 0xFFFFFFF0u;    // past the range: the copy reads zeros
 
 template <bool KMAJOR>
 __device__ __forceinline__ Src make_src(Operand op, int mn0, int k_begin, int MN, int k_end, int wave, int lane) {
   Src s;
+  // (k_begin is a multiple of BK = 32 and mn0 of 256, so blocked stages and
+  // tiles start on a 32-block.)
+  const bf16* base;
+  if (KMAJOR)
+    base = op.blk ? op.p + ((int64_t)(k_begin >> 5) * op.blk + mn0) * 32 : op.p + (int64_t)mn0 * op.ld + k_begin;
+  else
+    base = op.blk ? op.p + ((int64_t)(mn0 >> 5) * op.blk + k_begin) * 32 : op.p + (int64_t)k_begin * op.ld + mn0;
+  s.base = (const char*)base;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int blk = 2 * wave + j;
@@ -108,33 +126,30 @@ __device__ __forceinline__ Src make_src(Operand op, int mn0, int k_begin, int MN
       const int row = blk * 16 + (lane >> 2);
       const int c = (lane & 3) ^ ((row >> 2) & 3);
       const int m = mn0 + row;
-      const int64_t mm = m < MN ? m : 0;
-      // (k_begin is a multiple of BK = 32, so blocked stages start on a block.)
-      s.base[j] = op.blk ? op.p + ((int64_t)(k_begin >> 5) * op.blk + mm) * 32 + 8 * c
-                         : op.p + mm * op.ld + k_begin + 8 * c;
+      s.off[j] = 2u * (uint32_t)(op.blk ? row * 32 + 8 * c : (int64_t)row * op.ld + 8 * c);
       const int rem = k_end - k_begin - 8 * c;
       s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
     } else {
       const int row = blk * 2 + (lane >> 5);
       const int c = (lane & 31) ^ (4 * (row & 3));
       const int m = mn0 + 8 * c;
-      const int64_t mm = m < MN ? m : 0;
-      s.base[j] = op.blk ? op.p + ((mm >> 5) * op.blk + k_begin + row) * 32 + (mm & 31)
-                         : op.p + (int64_t)(k_begin + row) * op.ld + mm;
+      s.off[j] = 2u * (uint32_t)(op.blk ? ((int64_t)(c >> 2) * op.blk + row) * 32 + 8 * (c & 3)
+                                        : (int64_t)row * op.ld + 8 * c);
       const int rem = k_end - k_begin - row;
       s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
     }
   }
-  s.step = op.blk ? (KMAJOR ? op.blk * 32 : (int64_t)BK * 32) : (KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld);
+  s.step = 2 * (op.blk ? (KMAJOR ? op.blk * 32 : (int64_t)BK * 32) : (KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld));
   return s;
 }
 
 __device__ __forceinline__ void issue(lds_t* slab, const Src& s, int kt, int wave) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(s.base + kt * s.step, kRsrcRange);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int blk = 2 * wave + j;
-    const bf16* src = kt < s.nvalid[j] ? s.base[j] + kt * s.step : (const bf16*)g_zero_chunk;
-    __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(slab + blk * 512), 16, 0, 0);
+    const uint32_t off = kt < s.nvalid[j] ? s.off[j] : kOffZero;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(slab + blk * 512), 16, off, 0, 0, 0);
   }
 }
 
@@ -177,6 +192,11 @@ __device__ __forceinline__ void colsum_frags(float* sum, const bf16x8 (&b0)[2], 
 #define GEMM_WAIT_VM8_LGKM0() __builtin_amdgcn_s_waitcnt(0x0078)
 #define GEMM_WAIT_VM12_LGKM0() __builtin_amdgcn_s_waitcnt(0x007C)
 #define GEMM_WAIT_VM0_LGKM0() __builtin_amdgcn_s_waitcnt(0x0070)
+// Keeps the compiler's scheduler from moving instructions across this point:
+// the fragment reads of one half-stage stay ahead of the other half's MFMAs
+// (left to itself it sinks each read next to its first use and then waits
+// for it with lgkmcnt(0)).
+#define GEMM_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 struct Ctx {
   Src sa, sb;
@@ -212,7 +232,9 @@ __device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, 
                                      float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
   bf16x8 a1[4], b1[2];
   read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
+  GEMM_SCHED_FENCE();
   mma_half(acc, a0, b0);
+  GEMM_SCHED_FENCE();
   // After the MFMAs are issued, so the sums run beside them.
   // colsum_r = kt % colsum_period, kept as a running count (no division).
   if (kColSum && colsum_period) {
@@ -223,7 +245,9 @@ __device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, 
   wg_barrier();
   fill(stage_ptr<S>(), c, kt + 4);
   read_half<AK, BKM>(a0, b0, stage_ptr<(S + 1) % 4>(), 0, c);
+  GEMM_SCHED_FENCE();
   mma_half(acc, a1, b1);
+  GEMM_SCHED_FENCE();
 }
 
 // acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
@@ -274,12 +298,16 @@ __device__ __forceinline__ void step_fill(f32x16 (&acc)[4][2], const Ctx& c, con
                                           bf16x8 (&b0)[2]) {
   bf16x8 a1[4], b1[2];
   read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
+  GEMM_SCHED_FENCE();
   mma_half(acc, a0, b0);
+  GEMM_SCHED_FENCE();
   GEMM_WAIT_VM8_LGKM0();
   wg_barrier();
   fill(stage_ptr<S>(), fc, fkt);
   if (kReadNext) read_half<AK, BKM>(a0, b0, stage_ptr<(S + 1) % 4>(), 0, c);
+  GEMM_SCHED_FENCE();
   mma_half(acc, a1, b1);
+  GEMM_SCHED_FENCE();
 }
 
 // Persistent form of mainloop for K a multiple of 4*BK (every tile then
@@ -344,6 +372,188 @@ __device__ __forceinline__ void persistent(Operand A, Operand B, int M, int N, i
     tn = tn_n;
     c = cn;
     read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
+  }
+  GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
+}
+
+// ---- ping-pong main loop ----
+//
+// The eight waves form two groups, g = wave / 4, with one wave of each group
+// on every SIMD.  The groups take turns: while one issues the 16 MFMAs of a
+// stage, the other reads the next stage's fragments from LDS and issues its
+// share of the copies, and a barrier between the phases hands the matrix
+// core to the other group.  The fragment reads and copies of one wave thus
+// overlap the other wave's MFMAs instead of both waves reading, then both
+// multiplying.  Group 0 copies the A slabs and group 1 the B slabs (each wave
+// 4 KB of one operand per stage).  With phase p = 2t + h, stage t is read by
+// group 0 in phase 2t - 1 and by group 1 in phase 2t, and multiplied in phases
+// 2t and 2t + 1.  Group 0 refills the A half of stage t's buffer with stage
+// t + 4 in phase 2t + 1 and group 1 the B half of stage t - 1's buffer with
+// stage t + 3 in phase 2t; each memory phase ends waiting for the group's
+// copies of the stage read next (vmcnt(8): the two younger stages stay in
+// flight) and for its fragment reads, so the following barrier publishes
+// both.
+
+struct Src4 {
+  const char* base;
+  int64_t step;
+  uint32_t off[4];
+  int nvalid[4];
+};
+
+// As make_src, for the four 1 KB blocks 4 wq .. 4 wq + 3 of a 16 KB slab.
+template <bool KMAJOR>
+__device__ __forceinline__ Src4 make_src4(Operand op, int mn0, int k_begin, int MN, int k_end, int wq, int lane) {
+  Src4 s;
+  const bf16* base;
+  if (KMAJOR)
+    base = op.blk ? op.p + ((int64_t)(k_begin >> 5) * op.blk + mn0) * 32 : op.p + (int64_t)mn0 * op.ld + k_begin;
+  else
+    base = op.blk ? op.p + ((int64_t)(mn0 >> 5) * op.blk + k_begin) * 32 : op.p + (int64_t)k_begin * op.ld + mn0;
+  s.base = (const char*)base;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int blk = 4 * wq + j;
+    if (KMAJOR) {
+      const int row = blk * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ ((row >> 2) & 3);
+      const int m = mn0 + row;
+      s.off[j] = 2u * (uint32_t)(op.blk ? row * 32 + 8 * c : (int64_t)row * op.ld + 8 * c);
+      const int rem = k_end - k_begin - 8 * c;
+      s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
+    } else {
+      const int row = blk * 2 + (lane >> 5);
+      const int c = (lane & 31) ^ (4 * (row & 3));
+      const int m = mn0 + 8 * c;
+      s.off[j] = 2u * (uint32_t)(op.blk ? ((int64_t)(c >> 2) * op.blk + row) * 32 + 8 * (c & 3)
+                                        : (int64_t)row * op.ld + 8 * c);
+      const int rem = k_end - k_begin - row;
+      s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
+    }
+  }
+  s.step = 2 * (op.blk ? (KMAJOR ? op.blk * 32 : (int64_t)BK * 32) : (KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld));
+  return s;
+}
+
+__device__ __forceinline__ void issue4(lds_t* slab, const Src4& s, int kt, int wq) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(s.base + kt * s.step, kRsrcRange);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int blk = 4 * wq + j;
+    const uint32_t off = kt < s.nvalid[j] ? s.off[j] : kOffZero;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(slab + blk * 512), 16, off, 0, 0, 0);
+  }
+}
+
+struct Frags {
+  bf16x8 a0[4], b0[2], a1[4], b1[2];
+};
+
+template <bool AK, bool BKM>
+__device__ __forceinline__ void read_stage(Frags& f, const lds_t* st, const Ctx& c) {
+  read_half<AK, BKM>(f.a0, f.b0, st, 0, c);
+  read_half<AK, BKM>(f.a1, f.b1, st, 1, c);
+}
+
+__device__ __forceinline__ void mma_stage(f32x16 (&acc)[4][2], const Frags& f) {
+  mma_half(acc, f.a0, f.b0);
+  mma_half(acc, f.a1, f.b1);
+}
+
+// A phase boundary: the barrier, with the scheduler kept from moving MFMAs or
+// fragment reads across it.
+__device__ __forceinline__ void pp_barrier() {
+  GEMM_SCHED_FENCE();
+  wg_barrier();
+  GEMM_SCHED_FENCE();
+}
+
+// Group 0, stage t in buffer S: multiply stage t, then read stage t + 1 and
+// copy the A half of stage t + 4 into buffer S.
+template <bool AK, bool BKM, bool kColSum, int S>
+__device__ __forceinline__ void pp_unit0(f32x16 (&acc)[4][2], Frags& f, const Ctx& c, const Src4& s, int t, int nk,
+                                         float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
+  mma_stage(acc, f);
+  if (kColSum && colsum_period) {
+    if (colsum_r == colsum_phase && (c.wave & 1) == 0) colsum_frags(colsum, f.b0, f.b1);
+    colsum_r = colsum_r + 1 == colsum_period ? 0 : colsum_r + 1;
+  }
+  pp_barrier();
+  // Unconditional: past the K range the copies read zeros and the reads are
+  // unused, and straight-line code keeps the compiler's wait counts exact.
+  issue4(stage_ptr<S>(), s, t + 4, c.wave & 3);
+  read_stage<AK, BKM>(f, stage_ptr<(S + 1) % 4>(), c);
+  GEMM_WAIT_VM8_LGKM0();
+  pp_barrier();
+}
+
+// Group 1, stage t in buffer S: copy the B half of stage t + 3 into buffer
+// S - 1, read stage t, then multiply it.
+template <bool AK, bool BKM, bool kColSum, int S>
+__device__ __forceinline__ void pp_unit1(f32x16 (&acc)[4][2], Frags& f, const Ctx& c, const Src4& s, int t, int nk,
+                                         float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
+  issue4(stage_ptr<(S + 3) % 4>() + OPE, s, t + 3, c.wave & 3);
+  read_stage<AK, BKM>(f, stage_ptr<S>(), c);
+  GEMM_WAIT_VM8_LGKM0();
+  pp_barrier();
+  mma_stage(acc, f);
+  if (kColSum && colsum_period) {
+    if (colsum_r == colsum_phase && (c.wave & 1) == 0) colsum_frags(colsum, f.b0, f.b1);
+    colsum_r = colsum_r + 1 == colsum_period ? 0 : colsum_r + 1;
+  }
+  pp_barrier();
+}
+
+// Same contract as mainloop (accumulator layout, colsum, K range); on return
+// no copy into the stage arrays is in flight, but other waves may still read
+// the last stage: barrier before reusing them.
+template <bool AK, bool BKM, bool kColSum = false>
+__device__ __forceinline__ void mainloop_pp(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
+                                            int k_end, int tm0, int tn0, float* colsum = nullptr,
+                                            int colsum_period = 0, int colsum_phase = 0) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = wave >> 2, wq = wave & 3;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
+  const int nk_real = (k_end - k_begin + BK - 1) / BK;
+  if (nk_real <= 0) return;
+  // Whole groups of four stages: the stages past the K range read zeros and
+  // add nothing, and the loop body stays free of conditions.
+  const int nk = (nk_real + 3) & ~3;
+  const Ctx c{Src{}, Src{}, 128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid};
+  int colsum_r = 0;
+  Frags f;
+  if (g == 0) {
+    const Src4 s = make_src4<AK>(A, tm0, k_begin, M, k_end, wq, lane);
+    issue4(stage_ptr<0>(), s, 0, wq);
+    issue4(stage_ptr<1>(), s, 1, wq);
+    issue4(stage_ptr<2>(), s, 2, wq);
+    issue4(stage_ptr<3>(), s, 3, wq);
+    GEMM_WAIT_VM8_LGKM0();  // A halves of stages 0 and 1
+    pp_barrier();
+    read_stage<AK, BKM>(f, stage_ptr<0>(), c);
+    GEMM_WAIT_VM8_LGKM0();
+    for (int t = 0; t < nk; t += 4) {
+      pp_unit0<AK, BKM, kColSum, 0>(acc, f, c, s, t, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit0<AK, BKM, kColSum, 1>(acc, f, c, s, t + 1, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit0<AK, BKM, kColSum, 2>(acc, f, c, s, t + 2, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit0<AK, BKM, kColSum, 3>(acc, f, c, s, t + 3, nk, colsum, colsum_period, colsum_phase, colsum_r);
+    }
+  } else {
+    const Src4 s = make_src4<BKM>(B, tn0, k_begin, N, k_end, wq, lane);
+    issue4(stage_ptr<0>() + OPE, s, 0, wq);
+    issue4(stage_ptr<1>() + OPE, s, 1, wq);
+    issue4(stage_ptr<2>() + OPE, s, 2, wq);
+    GEMM_WAIT_VM8_LGKM0();  // B half of stage 0
+    pp_barrier();
+    for (int t = 0; t < nk; t += 4) {
+      pp_unit1<AK, BKM, kColSum, 0>(acc, f, c, s, t, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit1<AK, BKM, kColSum, 1>(acc, f, c, s, t + 1, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit1<AK, BKM, kColSum, 2>(acc, f, c, s, t + 2, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit1<AK, BKM, kColSum, 3>(acc, f, c, s, t + 3, nk, colsum, colsum_period, colsum_phase, colsum_r);
+    }
   }
   GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
 }

@@ -39,6 +39,10 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_rmsnorm_bwd": (I, [P, P, P, P, P, P, P, I, P, Z, I, I, P]),
     "gptrig_bias_grad": (I, [P, I, I, P, P]),
     "gptrig_weight_grad": (I, [P, P, P, P, I, I, I, P]),
+    "gptrig_linear": (I, [P, L, P, L, I, P, P, L, I, I, I, P]),
+    "gptrig_linear_gelu": (I, [P, L, P, L, I, P, P, P, L, I, I, I, P]),
+    "gptrig_linear_rope": (I, [P, L, P, L, I, P, P, L, I, I, I, P, P, I, I, I, P]),
+    "gptrig_linear_dgelu": (I, [P, L, P, L, I, P, L, P, L, I, I, I, P]),
     "gptrig_gelu_fwd": (I, [P, P, L, P]),
     "gptrig_gelu_bwd": (I, [P, P, P, L, P]),
     "gptrig_rope_table": (I, [P, P, I, I, P]),

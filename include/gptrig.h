@@ -134,6 +134,38 @@ int gptrig_weight_grad(const void* x, const void* dy, float* dw, float* db, int 
  * dy bf16 [rows, cols] (cols % 8 == 0). */
 int gptrig_bias_grad(const void* dy, int rows, int cols, float* db, void* stream);
 
+/* Dense linear layer, rig/nn.py:55-56 (linear(x, w, b) = bf16(x w) + b):
+ * y bf16 [n, f] (row stride ldy) = bf16(bf16(x w) + bias) for x bf16 [n, k]
+ * (row stride ldx) and bias bf16 [f] (NULL: no bias, y = bf16(x w)).  The
+ * weight is w [k, f] (w_kmajor = 0, the reference's layout, row stride ldw)
+ * or its transpose [f, k] (w_kmajor = 1), which the kernel reads faster; an
+ * input gradient dx = dy w^T is gptrig_linear(dy, w as [f = d_in, k = d_out],
+ * w_kmajor = 1, bias NULL).  k, f, ldx, ldw multiples of 8, ldy of 4; x and w
+ * 16-byte aligned, y 8-byte aligned. */
+int gptrig_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_kmajor, const void* bias, void* y,
+                  int64_t ldy, int n, int k, int f, void* stream);
+/* The MLP up-projection and its GELU (recipes/reference/train.py:1170-1171):
+ * h = linear(x, w, b) as gptrig_linear, g = bf16(gelu_tanh(h)), both [n, f]
+ * with row stride ldy (h is kept for the backward). */
+int gptrig_linear_gelu(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_kmajor, const void* bias,
+                       void* h, void* g, int64_t ldy, int n, int k, int f, void* stream);
+/* The QKV projection and the RoPE of q and k (recipes/reference/train.py:
+ * 1136-1142, rig/nn.py:36-52): y = linear(x, w, b) as gptrig_linear, then
+ * columns [0, rope_cols) rotated as gptrig_rope_fwd does (head_dim-wide
+ * groups, position = row % seq, tables from gptrig_rope_table; head_dim % 4
+ * == 0, rope_cols a multiple of head_dim). */
+int gptrig_linear_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_kmajor, const void* bias,
+                       void* y, int64_t ldy, int n, int k, int f, const void* cos_table, const void* sin_table,
+                       int seq, int rope_cols, int head_dim, void* stream);
+/* Input gradient of the down-projection times the GELU VJP (the backward of
+ * recipes/reference/train.py:1171-1173): dx bf16 [n, f] = bf16(bf16(dy w^T) *
+ * gelu_tanh'(h)), dy bf16 [n, k], w as in gptrig_linear ([f, k] with
+ * w_kmajor = 1 is the reference's [d_in, d_out] weight), h bf16 [n, f] the
+ * saved pre-activation (row stride ldh); equal to gptrig_linear then
+ * gptrig_gelu_bwd on the same GEMM output. */
+int gptrig_linear_dgelu(const void* dy, int64_t lddy, const void* w, int64_t ldw, int w_kmajor, const void* h,
+                        int64_t ldh, void* dx, int64_t lddx, int n, int k, int f, void* stream);
+
 /* GELU, tanh approximation: jax.nn.gelu(approximate=True) at
  * recipes/reference/train.py:1171.  bf16 [n]. */
 int gptrig_gelu_fwd(const void* x, void* y, int64_t n, void* stream);

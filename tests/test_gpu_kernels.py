@@ -477,3 +477,121 @@ def test_transpose_bf16_bit_exact():
         _lib.call("gptrig_transpose_bf16", xg.data_ptr(), out.data_ptr(), rows, cols, _lib.stream())
         torch.cuda.synchronize()
         assert torch.equal(out.cpu(), x.t().contiguous())
+
+
+# --- dense linear layers with fused epilogues -------------------------------------
+
+LINEAR_CASES = [
+    # (n, k, f, w_kmajor): the persistent form (k % 128 == 0, weight stored
+    # [f, k]) and the per-tile form, ragged token and feature counts.
+    (1000, 768, 264, 1),
+    (300, 200, 136, 1),
+    (513, 256, 520, 0),
+    (2048, 3072, 768, 1),
+]
+
+
+def _linear_call(fn, x, w, w_kmajor, *rest):
+    from gptrig import _lib
+
+    n, k = x.shape
+    ldw = k if w_kmajor else w.shape[1]
+    return _lib.call(fn, x.data_ptr(), k, w.data_ptr(), ldw, w_kmajor, *rest)
+
+
+def _dev_weight(w, w_kmajor):
+    """w [k, f] as the reference stores it; the kernel reads [f, k] when w_kmajor."""
+    return (w.t().contiguous() if w_kmajor else w).to(DEV)
+
+
+@pytest.mark.parametrize("n,k,f,w_kmajor", LINEAR_CASES)
+def test_linear_matches_oracle(n, k, f, w_kmajor):
+    """gptrig_linear against oracle.nn.linear (rig/nn.py:55-56): the product
+    rounded to bf16, then the bias add rounded.  The two fp32 products differ
+    only in summation order, so results agree to one rounding step of each of
+    the two roundings, and almost all elements bit for bit."""
+    from gptrig import _lib
+
+    print(f"linear n={n} k={k} f={f} w_kmajor={w_kmajor}", flush=True)
+    x, w, b = randn((n, k), 131), randn((k, f), 132, 0.05), randn((f,), 133, 0.1)
+    want = onn.linear(x, w, b, torch.bfloat16).float()
+    xg, wg, bg = x.to(DEV), _dev_weight(w, w_kmajor), b.to(DEV)
+    y = torch.full((n, f), float("nan"), dtype=torch.bfloat16, device=DEV)
+    _linear_call("gptrig_linear", xg, wg, w_kmajor, bg.data_ptr(), y.data_ptr(), f, n, k, f,
+                        _lib.stream())
+    got = y.float().cpu()
+    tol = 2 ** -7 * (2 * want.abs() + b.float().abs()) + 1e-6
+    assert bool(((got - want).abs() <= tol).all()), float((got - want).abs().max())
+    assert float((got != want).float().mean()) < 0.02
+    # Without a bias: the input-gradient form dx = dy w^T, one rounding.
+    y.fill_(float("nan"))
+    _linear_call("gptrig_linear", xg, wg, w_kmajor, None, y.data_ptr(), f, n, k, f, _lib.stream())
+    want0 = (x.float() @ w.float()).to(torch.bfloat16).float()
+    got0 = y.float().cpu()
+    assert bool(((got0 - want0).abs() <= 2 ** -7 * want0.abs() + 1e-6).all())
+    assert float((got0 != want0).float().mean()) < 0.02
+
+
+@pytest.mark.parametrize("n,k,f,w_kmajor", [(1000, 768, 768, 1), (300, 200, 256, 1), (513, 256, 512, 0)])
+def test_linear_epilogues_equal_separate_passes(n, k, f, w_kmajor):
+    """The fused epilogues give, bit for bit, what the separate passes give on
+    the same GEMM output: linear_gelu = (linear, gelu_fwd), linear_rope =
+    (linear, rope_fwd on the first rope_cols columns), linear_dgelu = (linear
+    without bias, gelu_bwd)."""
+    from gptrig import _lib
+    from gptrig import nn as gnn
+
+    print(f"linear epilogues n={n} k={k} f={f} w_kmajor={w_kmajor}", flush=True)
+    s = _lib.stream()
+    x, w, b = randn((n, k), 141), randn((k, f), 142, 0.05), randn((f,), 143, 0.1)
+    hsv = randn((n, f), 144, 2.0)
+    xg, wg, bg, hg = x.to(DEV), _dev_weight(w, w_kmajor), b.to(DEV), hsv.to(DEV)
+    new = lambda: torch.full((n, f), float("nan"), dtype=torch.bfloat16, device=DEV)
+    base, base0 = new(), new()
+    _linear_call("gptrig_linear", xg, wg, w_kmajor, bg.data_ptr(), base.data_ptr(), f, n, k, f, s)
+    _linear_call("gptrig_linear", xg, wg, w_kmajor, None, base0.data_ptr(), f, n, k, f, s)
+
+    h, g = new(), new()
+    _linear_call("gptrig_linear_gelu", xg, wg, w_kmajor, bg.data_ptr(), h.data_ptr(), g.data_ptr(), f, n, k,
+                        f, s)
+    g_two = new()
+    _lib.call("gptrig_gelu_fwd", base.data_ptr(), g_two.data_ptr(), n * f, s)
+    assert torch.equal(h.cpu(), base.cpu())
+    assert torch.equal(g.cpu(), g_two.cpu())
+
+    seq, head_dim = 100, 64
+    rope_cols = (f // 2) // head_dim * head_dim
+    c, sn = gnn.rope_tables(seq, head_dim, torch.device(DEV))
+    yr = new()
+    _linear_call("gptrig_linear_rope", xg, wg, w_kmajor, bg.data_ptr(), yr.data_ptr(), f, n, k, f,
+                        c.data_ptr(), sn.data_ptr(), seq, rope_cols, head_dim, s)
+    r_two = base.clone()
+    gnn.rope_inplace(r_two, f, n, seq, rope_cols // head_dim, head_dim)
+    assert torch.equal(yr.cpu(), r_two.cpu())
+    assert torch.equal(yr[:, rope_cols:].cpu(), base[:, rope_cols:].cpu())
+
+    dx = new()
+    _linear_call("gptrig_linear_dgelu", xg, wg, w_kmajor, hg.data_ptr(), f, dx.data_ptr(), f, n, k, f, s)
+    dx_two = new()
+    _lib.call("gptrig_gelu_bwd", base0.data_ptr(), hg.data_ptr(), dx_two.data_ptr(), n * f, s)
+    assert torch.equal(dx.cpu(), dx_two.cpu())
+
+
+def test_linear_rejects_bad_shapes():
+    from gptrig import _lib
+
+    x = torch.zeros((64, 72), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((64, 72), dtype=torch.bfloat16, device=DEV)
+    y = torch.zeros((64, 64), dtype=torch.bfloat16, device=DEV)
+    s = _lib.stream()
+    bad = [
+        ("gptrig_linear", x.data_ptr(), 72, w.data_ptr(), 72, 1, None, y.data_ptr(), 64, 64, 70, 64, s),  # k % 8
+        ("gptrig_linear", x.data_ptr(), 72, w.data_ptr(), 72, 1, None, y.data_ptr(), 64, 64, 72, 60, s),  # f % 8
+        ("gptrig_linear", x.data_ptr() + 2, 72, w.data_ptr(), 72, 1, None, y.data_ptr(), 64, 64, 72, 64, s),
+        ("gptrig_linear_rope", x.data_ptr(), 72, w.data_ptr(), 72, 1, None, y.data_ptr(), 64, 64, 72, 64,
+         w.data_ptr(), w.data_ptr(), 16, 32, 62, s),  # head_dim % 4
+        ("gptrig_linear_dgelu", x.data_ptr(), 72, w.data_ptr(), 72, 1, None, 64, y.data_ptr(), 64, 64, 72, 64, s),
+    ]
+    for args in bad:
+        with pytest.raises(RuntimeError):
+            _lib.call(*args)
