@@ -55,9 +55,11 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // GELU, tanh approximation (jax.nn.gelu(approximate=True)), in fp32.
 __device__ __forceinline__ float tanh_fast(float u) {
-  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-inf.
+  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-inf.  The
+  // reciprocal is v_rcp_f32 (1 ulp), not the IEEE division sequence: its error
+  // is far below the bf16 rounding of every caller's result.
   float e = fast_exp2(2.0f * GPTRIG_LOG2E * u);
-  return 1.0f - 2.0f / (e + 1.0f);
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
 }
 __device__ __forceinline__ float gelu_f(float x) {
   const float k = 0.7978845608028654f;  // sqrt(2/pi)

@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
   int tm, tn;
   gemm::tile_coords(blockIdx.x, V, N, tm, tn);
   f32x16 acc[4][2];
-  gemm::mainloop<true, true>(acc, W, Hd, V, N, 0, D, tm * BM, tn * BN);
+  gemm::mainloop_pp<true, true>(acc, W, Hd, V, N, 0, D, tm * BM, tn * BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
@@ -184,7 +184,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
   // than groups of 8 (the G^T stores compete with the operand slabs for L2).
   gemm::tile_coords(blockIdx.x, Vc, N, tm, tn, 2);
   f32x16 acc[4][2];
-  gemm::mainloop<true, true>(acc, W, Hd, Vc, N, 0, D, tm * BM, tn * BN);
+  gemm::mainloop_pp<true, true>(acc, W, Hd, Vc, N, 0, D, tm * BM, tn * BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;

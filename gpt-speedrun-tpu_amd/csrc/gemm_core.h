@@ -223,76 +223,11 @@ __device__ __forceinline__ void fill(lds_t* st, const Ctx& c, int kt) {
   issue(st + OPE, c.sb, kt, c.wave);
 }
 
-// One stage: on entry a0/b0 hold k-chunk 0 of stage kt (buffer S).  Reads
-// chunk 1, runs chunk 0's MFMAs, waits for stage kt+1 and the barrier (every
-// wave is done with buffer S), refills S with stage kt+4, reads chunk 0 of
-// stage kt+1, runs chunk 1's MFMAs.
-template <bool AK, bool BKM, bool kColSum, int S>
-__device__ __forceinline__ void step(f32x16 (&acc)[4][2], const Ctx& c, int kt, bf16x8 (&a0)[4], bf16x8 (&b0)[2],
-                                     float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
-  bf16x8 a1[4], b1[2];
-  read_half<AK, BKM>(a1, b1, stage_ptr<S>(), 1, c);
-  GEMM_SCHED_FENCE();
-  mma_half(acc, a0, b0);
-  GEMM_SCHED_FENCE();
-  // After the MFMAs are issued, so the sums run beside them.
-  // colsum_r = kt % colsum_period, kept as a running count (no division).
-  if (kColSum && colsum_period) {
-    if (colsum_r == colsum_phase && (c.wave & 1) == 0) colsum_frags(colsum, b0, b1);
-    colsum_r = colsum_r + 1 == colsum_period ? 0 : colsum_r + 1;
-  }
-  GEMM_WAIT_VM8_LGKM0();
-  wg_barrier();
-  fill(stage_ptr<S>(), c, kt + 4);
-  read_half<AK, BKM>(a0, b0, stage_ptr<(S + 1) % 4>(), 0, c);
-  GEMM_SCHED_FENCE();
-  mma_half(acc, a1, b1);
-  GEMM_SCHED_FENCE();
-}
-
-// acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
-// with wm0 = 128*(wave&1), wn0 = 64*(wave>>1); K range [k_begin, k_end).
-// With kColSum and colsum_period > 0, colsum[nb] (two floats per lane) also
-// accumulates, in the waves with wave % 2 == 0, the sums of B(k, tn0 + wn0 +
-// 32nb + lane%32) over this lane half's k of the stages kt of the K range
-// with kt % colsum_period == colsum_phase (see colsum_frags): the workgroups
-// that share a B slab split the sums between them.
-// Uses the four stage arrays; on return no copy into them is in flight, but
-// other waves may still read the last stage: barrier before reusing them.
-template <bool AK, bool BKM, bool kColSum = false>
-__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
-                                         int k_end, int tm0, int tn0, float* colsum = nullptr,
-                                         int colsum_period = 0, int colsum_phase = 0) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
-  const int nk = (k_end - k_begin + BK - 1) / BK;
-  if (nk <= 0) return;
-  const Ctx c{make_src<AK>(A, tm0, k_begin, M, k_end, wave, lane), make_src<BKM>(B, tn0, k_begin, N, k_end, wave, lane),
-              128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid};
-  fill(stage_ptr<0>(), c, 0);
-  fill(stage_ptr<1>(), c, 1);
-  fill(stage_ptr<2>(), c, 2);
-  fill(stage_ptr<3>(), c, 3);
-  GEMM_WAIT_VM12_LGKM0();
-  wg_barrier();
-  bf16x8 a0[4], b0[2];
-  read_half<AK, BKM>(a0, b0, stage_ptr<0>(), 0, c);
-  int colsum_r = 0;
-  for (int kt = 0; kt < nk; kt += 4) {
-    step<AK, BKM, kColSum, 0>(acc, c, kt, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
-    if (kt + 1 < nk) step<AK, BKM, kColSum, 1>(acc, c, kt + 1, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
-    if (kt + 2 < nk) step<AK, BKM, kColSum, 2>(acc, c, kt + 2, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
-    if (kt + 3 < nk) step<AK, BKM, kColSum, 3>(acc, c, kt + 3, a0, b0, colsum, colsum_period, colsum_phase, colsum_r);
-  }
-  GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends
-}
-
-// One stage of the persistent form: as step(), but the refill of buffer S
-// comes from `fc` at stage fkt (the next tile's sources once the current tile
-// has no stages left to copy).
+// One stage of the persistent form: on entry a0/b0 hold k-chunk 0 of stage kt
+// (buffer S).  Reads chunk 1, runs chunk 0's MFMAs, waits for stage kt+1 and
+// the barrier (every wave is done with buffer S), refills S from `fc` at
+// stage fkt (the current tile's stage kt+4, or one of the next tile's first
+// stages), reads chunk 0 of stage kt+1, runs chunk 1's MFMAs.
 template <bool AK, bool BKM, int S, bool kReadNext = true>
 __device__ __forceinline__ void step_fill(f32x16 (&acc)[4][2], const Ctx& c, const Ctx& fc, int fkt, bf16x8 (&a0)[4],
                                           bf16x8 (&b0)[2]) {
@@ -310,7 +245,7 @@ __device__ __forceinline__ void step_fill(f32x16 (&acc)[4][2], const Ctx& c, con
   GEMM_SCHED_FENCE();
 }
 
-// Persistent form of mainloop for K a multiple of 4*BK (every tile then
+// Persistent main loop for K a multiple of 4*BK (every tile then
 // starts at stage buffer 0): the workgroup runs tiles blockIdx.x,
 // blockIdx.x + gridDim.x, ... over the full K range, and the first four
 // stages of its next tile are copied during the last four stages of the
@@ -395,13 +330,19 @@ __device__ __forceinline__ void persistent(Operand A, Operand B, int M, int N, i
 // both.
 
 struct Src4 {
-  const char* base;
-  int64_t step;
-  uint32_t off[4];
-  int nvalid[4];
+  const char* base;  // uniform: the operand at the tile origin and k_begin
+  int64_t step;      // uniform: bytes per stage
+  uint32_t jstep2;   // uniform: bytes from the wave's block j to block j + 2
+  uint32_t off[2];   // lane: byte offsets of its chunks in blocks 0 and 1
+  int krem[2];       // lane: block j is inside the K range at stage kt iff 32 kt + kj j < krem[j % 2]
+  int rowlim;        // lane (K-major): block j is inside the M/N extent iff 16 j < rowlim
 };
 
-// As make_src, for the four 1 KB blocks 4 wq .. 4 wq + 3 of a 16 KB slab.
+// As make_src, for the four 1 KB blocks 4 wq .. 4 wq + 3 of a 16 KB slab, in
+// a compact form: blocks j and j + 2 of a wave differ by a fixed stride
+// (32 rows of a K-major slab, 4 k-rows of an MN-major one) and the same chunk
+// swizzle.  (In an MN-major slab the swizzle alternates between even and odd
+// blocks, whose k-rows 2j + lane/32 differ in bit 1.)
 template <bool KMAJOR>
 __device__ __forceinline__ Src4 make_src4(Operand op, int mn0, int k_begin, int MN, int k_end, int wq, int lane) {
   Src4 s;
@@ -411,37 +352,41 @@ __device__ __forceinline__ Src4 make_src4(Operand op, int mn0, int k_begin, int 
   else
     base = op.blk ? op.p + ((int64_t)(mn0 >> 5) * op.blk + k_begin) * 32 : op.p + (int64_t)k_begin * op.ld + mn0;
   s.base = (const char*)base;
+  if (KMAJOR) {
+    const int row = 64 * wq + (lane >> 2);        // block 0; block j adds 16 j rows
+    const int c = (lane & 3) ^ ((row >> 2) & 3);  // the same for the four blocks
+    const int64_t rs = op.blk ? 32 : op.ld;       // elements per row
+    s.off[0] = 2u * (uint32_t)(row * rs + 8 * c);
+    s.off[1] = s.off[0] + 2u * (uint32_t)(16 * rs);
+    s.jstep2 = 2u * (uint32_t)(32 * rs);
+    s.krem[0] = s.krem[1] = k_end - k_begin - 8 * c;
+    s.rowlim = MN - mn0 - row;
+  } else {
+    const int row0 = 8 * wq + (lane >> 5);  // block j holds k-row row0 + 2j
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int blk = 4 * wq + j;
-    if (KMAJOR) {
-      const int row = blk * 16 + (lane >> 2);
-      const int c = (lane & 3) ^ ((row >> 2) & 3);
-      const int m = mn0 + row;
-      s.off[j] = 2u * (uint32_t)(op.blk ? row * 32 + 8 * c : (int64_t)row * op.ld + 8 * c);
-      const int rem = k_end - k_begin - 8 * c;
-      s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
-    } else {
-      const int row = blk * 2 + (lane >> 5);
+    for (int p = 0; p < 2; ++p) {
+      const int row = row0 + 2 * p;
       const int c = (lane & 31) ^ (4 * (row & 3));
       const int m = mn0 + 8 * c;
-      s.off[j] = 2u * (uint32_t)(op.blk ? ((int64_t)(c >> 2) * op.blk + row) * 32 + 8 * (c & 3)
+      s.off[p] = 2u * (uint32_t)(op.blk ? ((int64_t)(c >> 2) * op.blk + row) * 32 + 8 * (c & 3)
                                         : (int64_t)row * op.ld + 8 * c);
-      const int rem = k_end - k_begin - row;
-      s.nvalid[j] = (m < MN && rem > 0) ? (rem + BK - 1) / BK : 0;
+      s.krem[p] = m < MN ? k_end - k_begin - row0 : 0;
     }
+    s.jstep2 = 2u * (uint32_t)(4 * (op.blk ? 32 : op.ld));
+    s.rowlim = 64;
   }
   s.step = 2 * (op.blk ? (KMAJOR ? op.blk * 32 : (int64_t)BK * 32) : (KMAJOR ? (int64_t)BK : (int64_t)BK * op.ld));
   return s;
 }
 
+template <bool KMAJOR>
 __device__ __forceinline__ void issue4(lds_t* slab, const Src4& s, int kt, int wq) {
   const __amdgpu_buffer_rsrc_t r = make_rsrc(s.base + kt * s.step, kRsrcRange);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int blk = 4 * wq + j;
-    const uint32_t off = kt < s.nvalid[j] ? s.off[j] : kOffZero;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(slab + blk * 512), 16, off, 0, 0, 0);
+    const bool ok = BK * kt + (KMAJOR ? 0 : 2 * j) < s.krem[j & 1] && (!KMAJOR || 16 * j < s.rowlim);
+    const uint32_t off = ok ? s.off[j & 1] + (j >> 1) * s.jstep2 : kOffZero;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(slab + (4 * wq + j) * 512), 16, off, 0, 0, 0);
   }
 }
 
@@ -468,11 +413,12 @@ __device__ __forceinline__ void pp_barrier() {
   GEMM_SCHED_FENCE();
 }
 
-// Group 0, stage t in buffer S: multiply stage t, then read stage t + 1 and
-// copy the A half of stage t + 4 into buffer S.
-template <bool AK, bool BKM, bool kColSum, int S>
-__device__ __forceinline__ void pp_unit0(f32x16 (&acc)[4][2], Frags& f, const Ctx& c, const Src4& s, int t, int nk,
-                                         float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
+// Group 0, stage t in buffer S: multiply stage t, then (memory phase) copy the
+// A half of stage dkt of `ds` into buffer S -- stage t + 4 of the stream --,
+// run mid(), and read stage t + 1 from buffer S + 1.
+template <bool AK, bool BKM, bool kColSum, int S, class Mid>
+__device__ __forceinline__ void pp_unit0(f32x16 (&acc)[4][2], Frags& f, const Ctx& c, const Src4& ds, int dkt,
+                                         float* colsum, int colsum_period, int colsum_phase, int& colsum_r, Mid mid) {
   mma_stage(acc, f);
   if (kColSum && colsum_period) {
     if (colsum_r == colsum_phase && (c.wave & 1) == 0) colsum_frags(colsum, f.b0, f.b1);
@@ -481,18 +427,21 @@ __device__ __forceinline__ void pp_unit0(f32x16 (&acc)[4][2], Frags& f, const Ct
   pp_barrier();
   // Unconditional: past the K range the copies read zeros and the reads are
   // unused, and straight-line code keeps the compiler's wait counts exact.
-  issue4(stage_ptr<S>(), s, t + 4, c.wave & 3);
+  issue4<AK>(stage_ptr<S>(), ds, dkt, c.wave & 3);
+  mid();
   read_stage<AK, BKM>(f, stage_ptr<(S + 1) % 4>(), c);
   GEMM_WAIT_VM8_LGKM0();
   pp_barrier();
 }
 
-// Group 1, stage t in buffer S: copy the B half of stage t + 3 into buffer
-// S - 1, read stage t, then multiply it.
-template <bool AK, bool BKM, bool kColSum, int S>
-__device__ __forceinline__ void pp_unit1(f32x16 (&acc)[4][2], Frags& f, const Ctx& c, const Src4& s, int t, int nk,
-                                         float* colsum, int colsum_period, int colsum_phase, int& colsum_r) {
-  issue4(stage_ptr<(S + 3) % 4>() + OPE, s, t + 3, c.wave & 3);
+// Group 1, stage t in buffer S: (memory phase) run mid(), copy the B half of
+// stage dkt of `ds` -- stage t + 3 of the stream -- into buffer S - 1, read
+// stage t; then multiply it.
+template <bool AK, bool BKM, bool kColSum, int S, class Mid>
+__device__ __forceinline__ void pp_unit1(f32x16 (&acc)[4][2], Frags& f, const Ctx& c, const Src4& ds, int dkt,
+                                         float* colsum, int colsum_period, int colsum_phase, int& colsum_r, Mid mid) {
+  mid();
+  issue4<BKM>(stage_ptr<(S + 3) % 4>() + OPE, ds, dkt, c.wave & 3);
   read_stage<AK, BKM>(f, stage_ptr<S>(), c);
   GEMM_WAIT_VM8_LGKM0();
   pp_barrier();
@@ -504,9 +453,19 @@ __device__ __forceinline__ void pp_unit1(f32x16 (&acc)[4][2], Frags& f, const Ct
   pp_barrier();
 }
 
-// Same contract as mainloop (accumulator layout, colsum, K range); on return
-// no copy into the stage arrays is in flight, but other waves may still read
-// the last stage: barrier before reusing them.
+struct NoMid {
+  __device__ __forceinline__ void operator()() const {}
+};
+
+// acc[mb][nb][i] = C[tm0 + wm0 + 32mb + 8(i/4) + 4(lane/32) + i%4][tn0 + wn0 + 32nb + lane%32]
+// with wm0 = 128*(wave&1), wn0 = 64*(wave>>1); K range [k_begin, k_end).
+// With kColSum and colsum_period > 0, colsum[nb] (two floats per lane) also
+// accumulates, in the waves with wave % 2 == 0, the sums of B(k, tn0 + wn0 +
+// 32nb + lane%32) over this lane half's k of the stages kt of the K range
+// with kt % colsum_period == colsum_phase (see colsum_frags): the workgroups
+// that share a B slab split the sums between them.
+// On return no copy into the stage arrays is in flight, but other waves may
+// still read the last stage: barrier before reusing them.
 template <bool AK, bool BKM, bool kColSum = false>
 __device__ __forceinline__ void mainloop_pp(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
                                             int k_end, int tm0, int tn0, float* colsum = nullptr,
@@ -527,32 +486,40 @@ __device__ __forceinline__ void mainloop_pp(f32x16 (&acc)[4][2], Operand A, Oper
   Frags f;
   if (g == 0) {
     const Src4 s = make_src4<AK>(A, tm0, k_begin, M, k_end, wq, lane);
-    issue4(stage_ptr<0>(), s, 0, wq);
-    issue4(stage_ptr<1>(), s, 1, wq);
-    issue4(stage_ptr<2>(), s, 2, wq);
-    issue4(stage_ptr<3>(), s, 3, wq);
+    issue4<AK>(stage_ptr<0>(), s, 0, wq);
+    issue4<AK>(stage_ptr<1>(), s, 1, wq);
+    issue4<AK>(stage_ptr<2>(), s, 2, wq);
+    issue4<AK>(stage_ptr<3>(), s, 3, wq);
     GEMM_WAIT_VM8_LGKM0();  // A halves of stages 0 and 1
     pp_barrier();
     read_stage<AK, BKM>(f, stage_ptr<0>(), c);
     GEMM_WAIT_VM8_LGKM0();
     for (int t = 0; t < nk; t += 4) {
-      pp_unit0<AK, BKM, kColSum, 0>(acc, f, c, s, t, nk, colsum, colsum_period, colsum_phase, colsum_r);
-      pp_unit0<AK, BKM, kColSum, 1>(acc, f, c, s, t + 1, nk, colsum, colsum_period, colsum_phase, colsum_r);
-      pp_unit0<AK, BKM, kColSum, 2>(acc, f, c, s, t + 2, nk, colsum, colsum_period, colsum_phase, colsum_r);
-      pp_unit0<AK, BKM, kColSum, 3>(acc, f, c, s, t + 3, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit0<AK, BKM, kColSum, 0>(acc, f, c, s, t + 4, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
+      pp_unit0<AK, BKM, kColSum, 1>(acc, f, c, s, t + 5, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
+      pp_unit0<AK, BKM, kColSum, 2>(acc, f, c, s, t + 6, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
+      pp_unit0<AK, BKM, kColSum, 3>(acc, f, c, s, t + 7, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
     }
   } else {
     const Src4 s = make_src4<BKM>(B, tn0, k_begin, N, k_end, wq, lane);
-    issue4(stage_ptr<0>() + OPE, s, 0, wq);
-    issue4(stage_ptr<1>() + OPE, s, 1, wq);
-    issue4(stage_ptr<2>() + OPE, s, 2, wq);
+    issue4<BKM>(stage_ptr<0>() + OPE, s, 0, wq);
+    issue4<BKM>(stage_ptr<1>() + OPE, s, 1, wq);
+    issue4<BKM>(stage_ptr<2>() + OPE, s, 2, wq);
     GEMM_WAIT_VM8_LGKM0();  // B half of stage 0
     pp_barrier();
     for (int t = 0; t < nk; t += 4) {
-      pp_unit1<AK, BKM, kColSum, 0>(acc, f, c, s, t, nk, colsum, colsum_period, colsum_phase, colsum_r);
-      pp_unit1<AK, BKM, kColSum, 1>(acc, f, c, s, t + 1, nk, colsum, colsum_period, colsum_phase, colsum_r);
-      pp_unit1<AK, BKM, kColSum, 2>(acc, f, c, s, t + 2, nk, colsum, colsum_period, colsum_phase, colsum_r);
-      pp_unit1<AK, BKM, kColSum, 3>(acc, f, c, s, t + 3, nk, colsum, colsum_period, colsum_phase, colsum_r);
+      pp_unit1<AK, BKM, kColSum, 0>(acc, f, c, s, t + 3, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
+      pp_unit1<AK, BKM, kColSum, 1>(acc, f, c, s, t + 4, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
+      pp_unit1<AK, BKM, kColSum, 2>(acc, f, c, s, t + 5, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
+      pp_unit1<AK, BKM, kColSum, 3>(acc, f, c, s, t + 6, colsum, colsum_period, colsum_phase, colsum_r,
+                                        NoMid{});
     }
   }
   GEMM_WAIT_VM0_LGKM0();  // no copy may land in LDS after the workgroup ends

@@ -189,7 +189,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
   gemm::Operand A{lhs + (int64_t)off * lda, lda};
   gemm::Operand B = kBT ? gemm::Operand{rhs + (int64_t)e * N * K, K} : gemm::Operand{rhs + (int64_t)e * K * N, N};
   f32x16 acc[4][2];
-  gemm::mainloop<true, kBT>(acc, A, B, cnt, N, 0, K, tm * gemm::BM, tn * gemm::BN);
+  gemm::mainloop_pp<true, kBT>(acc, A, B, cnt, N, 0, K, tm * gemm::BM, tn * gemm::BN);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
@@ -248,8 +248,8 @@ __global__ void __launch_bounds__(gemm::THREADS)
   f32x16 acc[4][2];
   float csum[2] = {0.f, 0.f};
   const bool do_colsum = db != nullptr;  // shared out over the M tiles
-  gemm::mainloop<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, csum,
-                                     do_colsum ? (K + gemm::BM - 1) / gemm::BM : 0, tm);
+  gemm::mainloop_pp<false, false, true>(acc, A, B, K, N, k_begin, k_end, tm * gemm::BM, tn * gemm::BN, csum,
+                                        do_colsum ? (K + gemm::BM - 1) / gemm::BM : 0, tm);
   const int hl = lane >> 5, l32 = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
   float* dwe = dw + (int64_t)e * K * N;

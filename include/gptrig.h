@@ -140,8 +140,8 @@ int gptrig_bias_grad(const void* dy, int rows, int cols, float* db, void* stream
  * weight is w [k, f] (w_kmajor = 0, the reference's layout, row stride ldw)
  * or its transpose [f, k] (w_kmajor = 1), which the kernel reads faster; an
  * input gradient dx = dy w^T is gptrig_linear(dy, w as [f = d_in, k = d_out],
- * w_kmajor = 1, bias NULL).  k, f, ldx, ldw multiples of 8, ldy of 4; x and w
- * 16-byte aligned, y 8-byte aligned. */
+ * w_kmajor = 1, bias NULL).  k, f, ldx, ldw, ldy multiples of 8; x, w and y
+ * 16-byte aligned. */
 int gptrig_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_kmajor, const void* bias, void* y,
                   int64_t ldy, int n, int k, int f, void* stream);
 /* The MLP up-projection and its GELU (recipes/reference/train.py:1170-1171):
@@ -152,7 +152,7 @@ int gptrig_linear_gelu(const void* x, int64_t ldx, const void* w, int64_t ldw, i
 /* The QKV projection and the RoPE of q and k (recipes/reference/train.py:
  * 1136-1142, rig/nn.py:36-52): y = linear(x, w, b) as gptrig_linear, then
  * columns [0, rope_cols) rotated as gptrig_rope_fwd does (head_dim-wide
- * groups, position = row % seq, tables from gptrig_rope_table; head_dim % 4
+ * groups, position = row % seq, tables from gptrig_rope_table; head_dim % 8
  * == 0, rope_cols a multiple of head_dim). */
 int gptrig_linear_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_kmajor, const void* bias,
                        void* y, int64_t ldy, int n, int k, int f, const void* cos_table, const void* sin_table,
@@ -161,8 +161,8 @@ int gptrig_linear_rope(const void* x, int64_t ldx, const void* w, int64_t ldw, i
  * recipes/reference/train.py:1171-1173): dx bf16 [n, f] = bf16(bf16(dy w^T) *
  * gelu_tanh'(h)), dy bf16 [n, k], w as in gptrig_linear ([f, k] with
  * w_kmajor = 1 is the reference's [d_in, d_out] weight), h bf16 [n, f] the
- * saved pre-activation (row stride ldh); equal to gptrig_linear then
- * gptrig_gelu_bwd on the same GEMM output. */
+ * saved pre-activation (row stride ldh, a multiple of 8, h 16-byte aligned);
+ * equal to gptrig_linear then gptrig_gelu_bwd on the same GEMM output. */
 int gptrig_linear_dgelu(const void* dy, int64_t lddy, const void* w, int64_t ldw, int w_kmajor, const void* h,
                         int64_t ldh, void* dx, int64_t lddx, int n, int k, int f, void* stream);
 
