@@ -530,6 +530,30 @@ __global__ void __launch_bounds__(256) weighted_sum_kernel(const float* __restri
   if (threadIdx.x == 0) atomicAdd(out, weight * (red[0] + red[1] + red[2] + red[3]));
 }
 
+// out[0] += sum(x * mask), out[1] += sum(mask): the masked loss sum and target
+// count of eval_step (recipes/reference/train.py:1519-1524), fp32 throughout
+// (an infinite loss under a zero mask gives NaN, as x * mask does there).
+__global__ void __launch_bounds__(256) masked_sum_kernel(const float* __restrict__ x, const float* __restrict__ mask,
+                                                         int64_t n, float* __restrict__ out) {
+  __shared__ float red[2][4];
+  float s = 0.f, c = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float m = mask[i];
+    s += x[i] * m;
+    c += m;
+  }
+  s = wave_sum(s);
+  c = wave_sum(c);
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x / 64] = s;
+    red[1][threadIdx.x / 64] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomicAdd(out, red[0][0] + red[0][1] + red[0][2] + red[0][3]);
+    atomicAdd(out + 1, red[1][0] + red[1][1] + red[1][2] + red[1][3]);
+  }
+}
 
 }  // namespace
 
@@ -788,6 +812,16 @@ int gptrig_weighted_sum(const float* x, int64_t n, float weight, float* out, voi
   int blocks = ceil_div(n, 256);
   if (blocks > 1024) blocks = 1024;
   weighted_sum_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(x, n, weight, out);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_masked_sum(const float* x, const float* mask, int64_t n, float* out, void* stream) {
+  if (!x || !mask || !out) return GPTRIG_E_NULL;
+  if (n <= 0) return GPTRIG_E_SHAPE;
+  int blocks = ceil_div(n, 256);
+  if (blocks > 1024) blocks = 1024;
+  masked_sum_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(x, mask, n, out);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

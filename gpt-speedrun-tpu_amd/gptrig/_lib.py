@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_transpose_bf16": (I, [P, P, I, I, P]),
     "gptrig_cast_f32_bf16": (I, [P, P, L, P]),
     "gptrig_weighted_sum": (I, [P, L, F, P, P]),
+    "gptrig_masked_sum": (I, [P, P, L, P, P]),
     "gptrig_fill_f32": (I, [P, L, F, P]),
     "gptrig_moe_route_workspace_bytes": (Z, [I, I, I]),
     "gptrig_moe_route": (I, [P, P, P, P, P, P, P, P, P, Z, I, I, I, P]),

@@ -253,28 +253,32 @@ class GPTTrainer:
         return _Ctx()
 
     # -- forward / backward of one micro-batch --------------------------------------
-    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float, micro: int) -> None:
+    def _forward(self, tokens: torch.Tensor, micro: int):
+        """Blocks and final norm of one micro-batch (``gpt_hidden``, ``train.py:1096-1176``).
+
+        Returns ``(tok, seg, x, xf, rstdf, saved)``: the flat int32 tokens, the
+        document segments (or ``None``), the last residual stream, its final
+        norm with the rstd, and each layer's saved activations.  The inputs of
+        the block linears go to this micro-batch's rows of ``lin_in``.
+        """
+
         c = self.config
         A = self.arena
         Bm, S = tokens.shape
         N, d, H, D = Bm * S, c.d_model, c.heads, c.head_dim
         rows = slice(micro * N, (micro + 1) * N)
         lin_in = [{k: t[rows] for k, t in layer.items()} for layer in self.lin_in]
-        lin_dout = [{k: t[rows] for k, t in layer.items()} for layer in self.lin_dout]
         stream = _lib.stream()
         tok = tokens.reshape(-1).to(torch.int32).contiguous()
-        tgt = targets.reshape(-1).to(torch.int32).contiguous()
         seg = document_segments(tokens, c.document_boundary_token).contiguous() if c.document_masking else None
 
         x = torch.empty((N, d), dtype=BF16, device=self.device)
         _lib.call("gptrig_embedding_fwd", tok.data_ptr(), A.w("token_embedding").data_ptr(), x.data_ptr(), N, d,
                   c.vocab_size, stream)
-        # strides (elements) of q/k/v inside the [N, 3d] projection, of o/do in [N, d]
+        # strides (elements) of q/k/v inside the [N, 3d] projection, of o in [N, d]
         st_qkv = (S * 3 * d, D, 3 * d)
         st_o = (S * d, D, d)
         attn_strides = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o], dtype=torch.int64)
-        bwd_strides = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o, *st_o, *st_qkv, *st_qkv, *st_qkv],
-                                   dtype=torch.int64)
         saved = []
         # Each residual add runs fused with the norm after it (ln2 of the same
         # block, ln1 of the next, or the final norm).
@@ -308,6 +312,22 @@ class GPTTrainer:
             x = x2
             if i + 1 < c.layers:
                 xn1, rstd1 = xn1_next, rstd1_next
+        return tok, seg, x, xf, rstdf, saved
+
+    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float, micro: int) -> None:
+        c = self.config
+        A = self.arena
+        Bm, S = tokens.shape
+        N, d, H, D = Bm * S, c.d_model, c.heads, c.head_dim
+        rows = slice(micro * N, (micro + 1) * N)
+        lin_dout = [{k: t[rows] for k, t in layer.items()} for layer in self.lin_dout]
+        stream = _lib.stream()
+        tgt = targets.reshape(-1).to(torch.int32).contiguous()
+        tok, seg, x, xf, rstdf, saved = self._forward(tokens, micro)
+        st_qkv = (S * 3 * d, D, 3 * d)
+        st_o = (S * d, D, d)
+        bwd_strides = torch.tensor([*st_qkv, *st_qkv, *st_qkv, *st_o, *st_o, *st_qkv, *st_qkv, *st_qkv],
+                                   dtype=torch.int64)
         head = A.w(self.head_path)
         losses = torch.empty(N, dtype=F32, device=self.device)
         lse_ce = torch.empty(N, dtype=F32, device=self.device)
@@ -422,6 +442,42 @@ class GPTTrainer:
                 _lib.call("gptrig_finalize_norm", self.sq_partials.data_ptr(), A.n_chunks, 0.0, self.norm.data_ptr(),
                           None, self.loss.data_ptr(), lr, _lib.ptr(row), stream)
             A.refresh_transposed()
+
+    def eval_step(self, x: torch.Tensor, y: torch.Tensor, mask: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Masked loss sum and target count (``eval_step``, ``train.py:1493-1525``, tiled loss).
+
+        ``x``, ``y``: int32 ``[batch, seq_len]`` tokens and targets, ``batch`` a
+        multiple of ``micro_batch_size`` up to ``batch_size``; ``mask`` the same
+        shape, any dtype (cast to float32).  Returns ``(sum(losses * mask),
+        sum(mask))`` as float32 device scalars, without a host sync.
+        """
+
+        c = self.config
+        shape = tuple(x.shape)
+        mb = c.micro_batch_size
+        if (len(shape) != 2 or shape[1] != c.seq_len or shape[0] % mb or shape[0] > c.batch_size
+                or tuple(y.shape) != shape or tuple(mask.shape) != shape):
+            raise ValueError(f"eval_step takes [k * {mb} <= {c.batch_size}, {c.seq_len}] tokens, targets and mask, "
+                             f"got {shape} / {tuple(y.shape)} / {tuple(mask.shape)}")
+        stream = _lib.stream()
+        out = torch.zeros(2, dtype=F32, device=self.device)
+        weights = mask.to(device=self.device, dtype=F32).contiguous()
+        head = self.arena.w(self.head_path)
+        for j in range(shape[0] // mb):
+            tokens = x[j * mb:(j + 1) * mb]
+            _, _, _, xf, _, _ = self._forward(tokens, j)
+            n = tokens.numel()
+            tgt = y[j * mb:(j + 1) * mb].reshape(-1).to(torch.int32).contiguous()
+            losses = torch.empty(n, dtype=F32, device=self.device)
+            lse = torch.empty(n, dtype=F32, device=self.device)
+            ws = self._workspace("flce_fwd", _lib.query("gptrig_flce_fwd_workspace_bytes", n, c.d_model,
+                                                        c.vocab_size))
+            _lib.call("gptrig_flce_fwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
+                      lse.data_ptr(), ws.data_ptr(), ws.numel(), n, c.d_model, c.vocab_size,
+                      c.semantic_vocab_size, stream)
+            _lib.call("gptrig_masked_sum", losses.data_ptr(), weights[j * mb:(j + 1) * mb].data_ptr(), n,
+                      out.data_ptr(), stream)
+        return out[0], out[1]
 
     def history_rows(self) -> np.ndarray:
         """Copy the on-device ``(loss, lr, grad_norm)`` history (one sync)."""

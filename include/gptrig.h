@@ -217,6 +217,9 @@ int gptrig_transpose_bf16(const void* src, void* dst, int rows, int cols, void* 
 /* Small helpers of the step: f32 -> bf16 cast, out += weight * sum(x), fill. */
 int gptrig_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream);
 int gptrig_weighted_sum(const float* x, int64_t n, float weight, float* out, void* stream);
+/* Masked loss sum of eval_step (recipes/reference/train.py:1493-1525):
+ * out[0] += sum(x * mask), out[1] += sum(mask), x and mask f32 [n]. */
+int gptrig_masked_sum(const float* x, const float* mask, int64_t n, float* out, void* stream);
 int gptrig_fill_f32(float* x, int64_t n, float value, void* stream);
 
 /* ------------------------------------------------------------------------

@@ -201,6 +201,20 @@ def cross_entropy(p: dict, x: torch.Tensor, y: torch.Tensor, config: Config) -> 
                                           vocab_tile_size=config.vocab_tile_size, compute_dtype=config.dtype)
 
 
+def eval_step(p: dict, x: torch.Tensor, y: torch.Tensor, mask: torch.Tensor,
+              config: Config) -> tuple[torch.Tensor, torch.Tensor]:
+    """``eval_step`` (``train.py:1493-1525``), tiled loss backend: the masked
+    loss sum and the target count, both float32."""
+
+    hidden = gpt_hidden(p, x, config)
+    head = p.get("output_embedding", p["token_embedding"])
+    losses = oflce.tiled_tied_cross_entropy_losses(hidden, head, y, semantic_vocab_size=config.semantic_vocab_size,
+                                                   vocab_tile_size=config.vocab_tile_size,
+                                                   compute_dtype=config.dtype)
+    weights = mask.to(F32)
+    return (losses * weights).sum(dtype=F32), weights.sum(dtype=F32)
+
+
 @dataclass
 class TrainState:
     params: dict

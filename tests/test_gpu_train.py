@@ -68,3 +68,27 @@ def test_initial_parameters_are_bit_identical_to_the_reference_draws():
     flat = om.flatten(om.init_params(ocfg, 3))
     for path, value in flat.items():
         assert torch.equal(trainer.arena.param(path).cpu(), torch.from_numpy(np.asarray(value))), path
+
+
+def test_eval_step_matches_oracle():
+    """eval_step (train.py:1493-1525) against the oracle's, from bit-identical
+    initial parameters: masked loss sum to 1e-3 relative, target count to fp32
+    summation order; one or two micro-batches; bad shapes raise."""
+    from gptrig.train import GPTTrainer
+
+    ocfg, gcfg = configs(1, 2)
+    trainer = GPTTrainer(gcfg, seed=0)
+    state = om.init_state(ocfg, 0)
+    w = torch.from_numpy(om.synthetic_windows(4, 1, 4, 128, 997)[0])
+    x, y = w[:, :-1], w[:, 1:]
+    g = torch.Generator().manual_seed(11)
+    mask = (torch.rand(x.shape, generator=g) < 0.7).float() * torch.rand(x.shape, generator=g)
+    for rows in (4, 2):
+        total, count = trainer.eval_step(x[:rows].cuda(), y[:rows].cuda(), mask[:rows].cuda())
+        want_total, want_count = om.eval_step(state.params, x[:rows], y[:rows], mask[:rows], ocfg)
+        print(f"eval rows={rows}: gpu {float(total):.6f} / {float(count):.3f}, "
+              f"oracle {float(want_total):.6f} / {float(want_count):.3f}", flush=True)
+        assert abs(float(total) - float(want_total)) <= 1e-3 * abs(float(want_total))
+        assert abs(float(count) - float(want_count)) <= 1e-5 * float(want_count)
+    with pytest.raises(ValueError):
+        trainer.eval_step(x[:3].cuda(), y[:3].cuda(), mask[:3].cuda())

@@ -168,6 +168,30 @@ def test_smoke_train_step_starts_near_uniform_loss():
 
 # --- routing ------------------------------------------------------------------
 
+def test_eval_step_masked_sum():
+    """eval_step (train.py:1493-1525): with an all-ones mask the loss sum over
+    the count is the training loss (cross_entropy's mean, a separate path
+    through the tiled losses); a zero mask gives (0, 0); the masked sum is
+    linear in the mask."""
+    cfg = om.smoke_config()
+    p = om.flatten(om.init_params(cfg, 5))
+    p = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in p.items()}
+    w = torch.from_numpy(om.synthetic_windows(3, 1, 2, 32, cfg.semantic_vocab_size)[0])
+    x, y = w[:, :-1], w[:, 1:]
+    total, count = om.eval_step(p, x, y, torch.ones(x.shape), cfg)
+    mean = om.cross_entropy(p, x, y, cfg)
+    assert float(count) == x.numel()
+    assert abs(float(total) / float(count) - float(mean)) <= 1e-6 * abs(float(mean))
+    zero = om.eval_step(p, x, y, torch.zeros(x.shape), cfg)
+    assert float(zero[0]) == 0.0 and float(zero[1]) == 0.0
+    g = torch.Generator().manual_seed(9)
+    m1 = (torch.rand(x.shape, generator=g) < 0.5).float()
+    m2 = torch.rand(x.shape, generator=g) * (1 - m1)
+    a, b, ab = (om.eval_step(p, x, y, m, cfg) for m in (m1, m2, m1 + m2))
+    assert abs(float(ab[0]) - float(a[0]) - float(b[0])) <= 1e-5 * abs(float(ab[0]))
+    assert abs(float(ab[1]) - float(a[1]) - float(b[1])) <= 1e-5 * float(ab[1])
+
+
 def test_top_k_brute_force_with_ties():
     rng = np.random.default_rng(0)
     logits = torch.from_numpy(rng.integers(-2, 3, size=(200, 6)).astype(np.float32))
