@@ -39,7 +39,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes.
-FLCE_TRAFFIC_BYTES = {32768: (17909 + 5159) * 2 ** 20, 65536: (35739 + 9071) * 2 ** 20}
+FLCE_TRAFFIC_BYTES = {32768: (17909 + 5159) * 2 ** 20, 65536: (35398 + 8258) * 2 ** 20}
 
 
 def parse_args():
@@ -64,6 +64,7 @@ def traffic_pass(micro_batch: int) -> None:
 
     from gptrig.kernels import flash_attention as fa
     from gptrig.kernels import linear_cross_entropy as lce
+    from gptrig.train import FLCE_CHUNK_PARTS
 
     dev = "cuda:0"
     torch.manual_seed(0)
@@ -75,7 +76,7 @@ def traffic_pass(micro_batch: int) -> None:
     w = (torch.randn(vocab, d, device=dev) * 0.02).bfloat16()
     t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32)
     _, lse = lce.flce_forward(h, w, t, vocab)
-    lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.chunk_for(-(-vocab // 3)))
+    lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.chunk_for(-(-vocab // FLCE_CHUNK_PARTS)))
     torch.cuda.synchronize()
     q, k, v, do = (torch.randn(micro_batch, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
     o, lse2 = fa.flash_forward(q, k, v, None, 0.125)

@@ -44,6 +44,9 @@ BLOCK_LEAVES = ("ln1_scale", "qkv_w", "qkv_b", "attn_w", "attn_b",
                 "ln2_scale", "mlp_up_w", "mlp_up_b", "mlp_down_w", "mlp_down_b")
 
 
+# Vocabulary chunks of the FLCE backward in the training step.
+FLCE_CHUNK_PARTS = 2
+
 @dataclass(frozen=True)
 class GPTConfig:
     """Model/optimizer fields of the reference ``Config`` (``train.py:176-282``)."""
@@ -339,9 +342,11 @@ class GPTTrainer:
         _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
 
         # ---- backward ----
-        # Three vocabulary chunks: the G^T workspace is a third of the logits'
-        # size, and the per-chunk dW GEMM is tall enough to need little K-split.
-        chunk = lce.chunk_for(max(c.vocab_tile_size, -(-c.vocab_size // 3)))
+        # Two vocabulary chunks: the G^T workspace is half the logits' size
+        # (3.3 GB at 65536 tokens), and the per-chunk GEMMs are long enough to
+        # need little K-split (measured 3% faster than three chunks, 0.3%
+        # slower than one).
+        chunk = lce.chunk_for(max(c.vocab_tile_size, -(-c.vocab_size // FLCE_CHUNK_PARTS)))
         ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
         dxf = torch.empty((N, d), dtype=BF16, device=self.device)
         with self._timed("flce"):
