@@ -39,7 +39,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes.
-FLCE_TRAFFIC_BYTES = {32768: (17909 + 5159) * 2 ** 20, 65536: (35398 + 8258) * 2 ** 20}
+FLCE_TRAFFIC_BYTES = {32768: (17909 + 5159) * 2 ** 20, 65536: (36120 + 8273) * 2 ** 20}
 
 
 def parse_args():
