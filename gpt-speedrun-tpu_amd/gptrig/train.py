@@ -488,3 +488,14 @@ class GPTTrainer:
         """Copy the on-device ``(loss, lr, grad_norm)`` history (one sync)."""
 
         return self.history[: self.step_count].cpu().numpy()
+
+    def write_training_log(self, output_dir, flops_per_token: float | None = None):
+        """Persist the curve so far as ``training.riglog`` (``rig/runlog.py:257-302``,
+        called once after the loop in ``train.py``); returns its path."""
+
+        from . import runlog
+
+        steps = min(self.step_count, self.history.shape[0])
+        return runlog.write_training_log(output_dir, self.history[:steps].cpu().numpy(),
+                                         tokens_per_step=self.config.batch_size * self.config.seq_len,
+                                         final_step=steps, flops_per_token=flops_per_token)

@@ -92,3 +92,68 @@ def test_eval_step_matches_oracle():
         assert abs(float(count) - float(want_count)) <= 1e-5 * float(want_count)
     with pytest.raises(ValueError):
         trainer.eval_step(x[:3].cuda(), y[:3].cuda(), mask[:3].cuda())
+
+
+def test_training_log_round_trips_the_device_history(tmp_path):
+    """An early-stopped run (3 of 6 steps) writes ``training.riglog`` with one
+    record per step taken, bit-equal to the on-device history (rig/runlog.py:257-302)."""
+    from gptrig import runlog
+    from gptrig.train import GPTTrainer
+
+    _, gcfg = configs(6, 2)
+    trainer = GPTTrainer(gcfg, seed=0)
+    windows = om.synthetic_windows(5, 3, 4, 128, 997)
+    for i in range(3):
+        w = torch.from_numpy(windows[i])
+        trainer.train_step(w[:, :-1].cuda(), w[:, 1:].cuda())
+    path = trainer.write_training_log(tmp_path, flops_per_token=1.0e6)
+    log = runlog.read_log(path)
+    rows = trainer.history_rows()
+    print("history", rows.tolist(), flush=True)
+    assert rows.shape == (3, 3) and np.all(rows[:, 0] > 0)
+    np.testing.assert_array_equal(log.steps, [1, 2, 3])
+    np.testing.assert_array_equal(log.values, rows)
+    np.testing.assert_array_equal(log.axis("tokens_processed"), np.arange(1, 4) * 4 * 128)
+    np.testing.assert_array_equal(log.axis("cumulative_flops"), np.arange(1, 4) * 4 * 128 * 1.0e6)
+
+
+def test_run_directory_is_what_the_harness_reads(tmp_path, capsys):
+    """``gptrig.run`` (train.py:run's artefacts and result line) on a tiny
+    config stopped at step 3 of 5: every artefact re-read and cross-checked."""
+    import json
+    import math
+
+    from test_runlog import harness_accepts
+
+    from gptrig import run as grun
+    from gptrig import runlog
+
+    config = ('{"layers": 2, "heads": 2, "d_model": 128, "vocab_size": 1000, "semantic_vocab_size": 997, '
+              '"seq_len": 128, "batch_size": 4, "micro_batch_size": 2, "base_width": 128, "base_depth": 2, '
+              '"optimizer": {"learning_rate": 0.00390625, "steps": 5, "warmup_steps": 1}}')
+    assert grun.main(["--output-dir", str(tmp_path), "--config", config, "--stop-after-step", "3"]) == 0
+    last = capsys.readouterr().out.strip().splitlines()[-1]
+    assert last.startswith(runlog.RESULT_PREFIX)
+    result = json.loads(last[len(runlog.RESULT_PREFIX):])
+    assert json.loads((tmp_path / "metrics.json").read_text()) == result
+    assert harness_accepts(result, tmp_path)
+    m = result["metrics"]
+    print({k: m[k] for k in ("train_seconds", "tokens_per_second", "validation_loss", "train_loss")}, flush=True)
+    assert m["training_steps"] == 3 and m["schedule_steps"] == 5 and m["tokens_processed"] == 3 * 4 * 128
+    assert m["validation_tokens"] == 4 * 128
+    assert abs(m["validation_loss"] - math.log(997)) < 0.5  # random init on uniform tokens
+
+    log = runlog.read_log(tmp_path / "training.riglog")
+    np.testing.assert_array_equal(log.steps, [1, 2, 3])
+    assert log.values[-1, 0] == np.float32(m["train_loss"])
+    assert log.flops_per_token == m["flops_per_token"] and log.tokens_per_step == 4 * 128
+    rows = (tmp_path / "validation.csv").read_text().splitlines()
+    assert rows[1].split(",")[:5] == ["3", str(3 * 512), "fineweb", "fineweb", "512"] and rows[1].endswith("true")
+    assert float(rows[1].split(",")[5]) == m["validation_loss"]
+
+    with np.load(tmp_path / "checkpoint.npz", allow_pickle=False) as z:
+        meta = json.loads(z["metadata.json"].tobytes().decode())
+        assert meta["model"]["layers"] == 2 and meta["seed"] == 0
+        names = [k for k in z.files if k.startswith("params/")]
+        assert sum(int(z[k].size) for k in names) == m["parameter_count"]
+        assert all(np.isfinite(z[k]).all() for k in names)
