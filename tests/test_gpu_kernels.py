@@ -78,6 +78,42 @@ def test_attention_forward_backward_matches_oracle(B, H, S, D, scale, segmented)
         assert maxabs(got, want) <= 2e-2
 
 
+def document_segments_of_lengths(sequence, seed):
+    """Segment ids of documents with lengths drawn from 1..3000 (some of length 1), as
+    ``document_segments`` assigns them to an 8k window of packed documents."""
+    rng = np.random.default_rng(seed)
+    lengths = []
+    while sum(lengths) < sequence:
+        lengths.append(int(rng.choice([1, 2, int(rng.integers(3, 300)), int(rng.integers(300, 3000))])))
+    seg = np.repeat(np.arange(len(lengths), dtype=np.int32), lengths)[:sequence]
+    return torch.from_numpy(seg[None].copy())
+
+
+@pytest.mark.parametrize("S,scale", [(8192, 1.0 / 64), (8000, None)])
+def test_attention_long_context_documents_match_oracle(S, scale):
+    """The 8k context preset (``recipes/reference/config.yaml:18-21``: seq 8192,
+    document masking, ``inverse_head_dim`` scale) and a non-128-aligned long
+    window, packed documents of 1..3000 tokens; tolerance 2e-2 x max(1, |ref|max)."""
+    from gptrig.kernels import flash_attention as fa
+
+    B, H, D = 1, 2, 64
+    print(f"attention long case S={S} scale={scale}", flush=True)
+    q, k, v, do = (randn((B, H, S, D), seed) for seed in (21, 22, 23, 24))
+    seg = document_segments_of_lengths(S, S)
+    sc = D ** -0.5 if scale is None else scale
+    o_ref, lse_ref = oattn.attention_forward(q, k, v, softmax_scale=sc, segment_ids=seg)
+    dq_ref, dk_ref, dv_ref = oattn.attention_backward(q, k, v, o_ref, lse_ref, do, softmax_scale=sc, segment_ids=seg)
+    qg, kg, vg, dog, segg = (t.to(DEV) for t in (q, k, v, do, seg))
+    o, lse = fa.flash_forward(qg, kg, vg, segg, sc)
+    dq, dk, dv = fa.flash_backward(qg, kg, vg, o_ref.to(DEV), lse_ref.to(DEV), dog, segg, sc)
+    torch.cuda.synchronize()
+    assert maxabs(lse, lse_ref) <= 2e-3
+    for name, got, want in (("o", o, o_ref), ("dq", dq, dq_ref), ("dk", dk, dk_ref), ("dv", dv, dv_ref)):
+        bound = 2e-2 * max(1.0, float(want.float().abs().max()))
+        print(f"  {name}: max|diff| {maxabs(got, want):.3e} bound {bound:.3e}", flush=True)
+        assert maxabs(got, want) <= bound, name
+
+
 def test_attention_autograd_api_and_strided_inputs():
     from gptrig.kernels import AttentionConfig, make_causal_attention
 
