@@ -34,12 +34,12 @@ import torch  # noqa: E402
 METRIC = "train tokens/s at 125M S=1024; attn-bwd + FLCE TFLOP/s as % of bf16 MFMA peak"
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # HBM bytes of one FLCE fwd+bwd launch sequence, by micro-batch tokens N (d 768,
-# V 50304, three vocabulary chunks): FETCH_SIZE (x 2.0, the factor the counter
+# V 50304, one vocabulary chunk): FETCH_SIZE (x 2.0, the factor the counter
 # reads for a 256 MiB copy) + WRITE_SIZE (x 1.0) summed over its launches, from
 # `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
-# changes.
-FLCE_TRAFFIC_BYTES = {32768: (17909 + 5159) * 2 ** 20, 65536: (36120 + 8273) * 2 ** 20}
+# changes; a shape without a measurement reports null.
+FLCE_TRAFFIC_BYTES = {65536: (35388 + 7636) * 2 ** 20}
 
 
 def parse_args():
@@ -50,6 +50,7 @@ def parse_args():
     ap.add_argument("--micro-batch", type=int, default=64,
                     help="sequences per forward/backward pass (the global batch of 128 is accumulated over 128 / micro-batch passes; 64 measured fastest: at 128 the attention working set outgrows the L2 + MALL)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention (B) and FLCE (C) configs")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="approximate CPU-baseline budget")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="run one 256 MiB calibration copy, one FLCE forward+backward and one attention "
@@ -64,8 +65,6 @@ def traffic_pass(micro_batch: int) -> None:
 
     from gptrig.kernels import flash_attention as fa
     from gptrig.kernels import linear_cross_entropy as lce
-    from gptrig.train import FLCE_CHUNK_PARTS
-
     dev = "cuda:0"
     torch.manual_seed(0)
     src = torch.randn(64 * 1024 * 1024, device=dev)  # 256 MiB: calibrates the counters
@@ -76,13 +75,77 @@ def traffic_pass(micro_batch: int) -> None:
     w = (torch.randn(vocab, d, device=dev) * 0.02).bfloat16()
     t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32)
     _, lse = lce.flce_forward(h, w, t, vocab)
-    lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.chunk_for(-(-vocab // FLCE_CHUNK_PARTS)))
+    lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.grad_chunk(n, vocab))
     torch.cuda.synchronize()
     q, k, v, do = (torch.randn(micro_batch, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
     o, lse2 = fa.flash_forward(q, k, v, None, 0.125)
     fa.flash_backward(q, k, v, o, lse2, do, None, 0.125)
     torch.cuda.synchronize()
     print("traffic pass done", flush=True)
+
+
+def isolated_configs(reps: int = 20) -> dict:
+    """The reference metric's isolated kernel configs, measured alone after the
+    step: B = causal attention fwd+bwd at B16 H12 S1024 D64 (q, k, v, dO ~ N(0,1)
+    from numpy seed 1, RoPE on q and k, scale 1/8) and C = FLCE fwd+bwd at
+    N16384 d768 V50304 (h ~ N(0,1), W ~ N(0,0.02), uniform targets).  Each
+    launch sequence is timed with HIP events on the stream it runs on,
+    averaged over ``reps`` after one untimed call."""
+
+    from gptrig import _lib
+    from gptrig.kernels import flash_attention as fa
+    from gptrig.kernels import linear_cross_entropy as lce
+    from gptrig.nn import apply_rotary
+
+    dev = "cuda:0"
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
+
+    assert _lib.stream() == torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(1)
+    B, H, S, D = 16, 12, 1024, 64
+    q, k, v, do = (torch.from_numpy(rng.standard_normal((B, H, S, D), dtype=np.float32)).to(dev).bfloat16()
+                   for _ in range(4))
+    q, k = (apply_rotary(t.transpose(1, 2).contiguous()).transpose(1, 2).contiguous() for t in (q, k))
+    o, lse = fa.flash_forward(q, k, v, None, 0.125)
+    fwd_ms = timed(lambda: fa.flash_forward(q, k, v, None, 0.125))
+    bwd_ms = timed(lambda: fa.flash_backward(q, k, v, o, lse, do, None, 0.125))
+    visible = S * (S + 1) // 2
+    fwd_tf = 4 * B * H * D * visible / (fwd_ms / 1e3) / 1e12
+    bwd_tf = attn_bwd_flops(B, H, S, D) / (bwd_ms / 1e3) / 1e12
+    del q, k, v, do, o, lse
+
+    n, d, vocab = 16384, 768, 50304
+    h = torch.from_numpy(rng.standard_normal((n, d), dtype=np.float32)).to(dev).bfloat16()
+    w = torch.from_numpy(rng.standard_normal((vocab, d), dtype=np.float32) * 0.02).to(dev).bfloat16()
+    t = torch.from_numpy(rng.integers(0, vocab, size=n, dtype=np.int32)).to(dev)
+    chunk = lce.grad_chunk(n, vocab)
+
+    def flce():
+        _, lse_c = lce.flce_forward(h, w, t, vocab)
+        lce.flce_backward(h, w, t, lse_c, None, 1.0 / n, vocab, chunk)
+
+    flce_ms = timed(flce)
+    flce_tf = flce_flops(n, d, vocab) / (flce_ms / 1e3) / 1e12
+    peak = MFMA_BF16_PEAK_TFLOPS
+    return {
+        "attention_B16_H12_S1024_D64": {
+            "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(fwd_tf, 1), "fwd_frac": round(fwd_tf / peak, 4),
+            "bwd_ms": round(bwd_ms, 4), "bwd_tflops": round(bwd_tf, 1), "bwd_frac": round(bwd_tf / peak, 4),
+            "bwd_algorithmic_flops": attn_bwd_flops(B, H, S, D)},
+        "flce_N16384_d768_V50304": {"ms": round(flce_ms, 4), "tflops": round(flce_tf, 1),
+                                    "frac": round(flce_tf / peak, 4), "algorithmic_flops": flce_flops(n, d, vocab)},
+    }
 
 
 def attn_bwd_flops(batch, heads, seq, head_dim):
@@ -241,6 +304,10 @@ def main():
         "adamw": {"ms": round(adam_ms, 3), "achieved_GBps": round(adam_gbs, 1), "peak_GBps": 8000},
         "loss_first_last": [float(hist[0, 0]), float(hist[-1, 0])],
     }
+    del trainer, windows, xs, ys
+    torch.cuda.empty_cache()
+    if not args.no_isolated:
+        result["isolated"] = isolated_configs()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -44,9 +44,6 @@ BLOCK_LEAVES = ("ln1_scale", "qkv_w", "qkv_b", "attn_w", "attn_b",
                 "ln2_scale", "mlp_up_w", "mlp_up_b", "mlp_down_w", "mlp_down_b")
 
 
-# Vocabulary chunks of the FLCE backward in the training step.
-FLCE_CHUNK_PARTS = 2
-
 @dataclass(frozen=True)
 class GPTConfig:
     """Model/optimizer fields of the reference ``Config`` (``train.py:176-282``)."""
@@ -342,11 +339,9 @@ class GPTTrainer:
         _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
 
         # ---- backward ----
-        # Two vocabulary chunks: the G^T workspace is half the logits' size
-        # (3.3 GB at 65536 tokens), and the per-chunk GEMMs are long enough to
-        # need little K-split (measured 3% faster than three chunks, 0.3%
-        # slower than one).
-        chunk = lce.chunk_for(max(c.vocab_tile_size, -(-c.vocab_size // FLCE_CHUNK_PARTS)))
+        # One vocabulary chunk while the bf16 G^T fits the budget (6.6 GB at
+        # 65536 tokens x 50304).
+        chunk = lce.grad_chunk(N, c.vocab_size)
         ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
         dxf = torch.empty((N, d), dtype=BF16, device=self.device)
         with self._timed("flce"):
