@@ -154,11 +154,14 @@ __device__ __forceinline__ void issue(lds_t* slab, const Src& s, int kt, int wav
 }
 
 // MFMA operand (8 k-values) for rows r0 .. r0+31 at k-chunk kc (0 or 1) of a slab.
+// K-major slabs: the lane reads row r0 + lrow (lrow = lane & 31 unless the
+// caller permutes the rows of the block; accumulator row m then belongs to the
+// slab row that lane m read).
 template <bool KMAJOR>
-__device__ __forceinline__ bf16x8 frag(const lds_t* slab, int r0, int kc, int lane) {
+__device__ __forceinline__ bf16x8 frag(const lds_t* slab, int r0, int kc, int lane, int lrow) {
   const int hl = lane >> 5;
   if (KMAJOR) {
-    const int row = r0 + (lane & 31);
+    const int row = r0 + lrow;
     const int c = 2 * kc + hl;
     return *(const lds_x8*)(slab + row * BK + 8 * (c ^ ((row >> 2) & 3)));
   } else {
@@ -201,14 +204,21 @@ __device__ __forceinline__ void colsum_frags(float* sum, const bf16x8 (&b0)[2], 
 struct Ctx {
   Src sa, sb;
   int wm0, wn0, wave, lane, tid;
+  int arow;  // row of each 32-row A block this lane reads (K-major A only; else lane & 31)
 };
+
+// The A-row order that gives lane (l32, hl) of a 32x32 accumulator the 16
+// consecutive rows 16 hl .. 16 hl + 15 as elements 0 .. 15: element i sits in
+// accumulator row 8 (i / 4) + 4 hl + i % 4, so lane l32 = 8a + 4h + b reads
+// slab row 16h + 4a + b.
+__device__ __forceinline__ int contiguous_row(int l32) { return 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3); }
 
 template <bool AK, bool BKM>
 __device__ __forceinline__ void read_half(bf16x8 (&a)[4], bf16x8 (&b)[2], const lds_t* st, int kc, const Ctx& c) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) a[mb] = frag<AK>(st, c.wm0 + 32 * mb, kc, c.lane);
+  for (int mb = 0; mb < 4; ++mb) a[mb] = frag<AK>(st, c.wm0 + 32 * mb, kc, c.lane, c.arow);
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) b[nb] = frag<BKM>(st + OPE, c.wn0 + 32 * nb, kc, c.lane);
+  for (int nb = 0; nb < 2; ++nb) b[nb] = frag<BKM>(st + OPE, c.wn0 + 32 * nb, kc, c.lane, c.lane & 31);
 }
 
 __device__ __forceinline__ void mma_half(f32x16 (&acc)[4][2], const bf16x8 (&a)[4], const bf16x8 (&b)[2]) {
@@ -254,17 +264,21 @@ __device__ __forceinline__ void step_fill(f32x16 (&acc)[4][2], const Ctx& c, con
 // before each tile's stages (after the previous tile's epilogue), e.g. to
 // prefetch per-tile epilogue inputs far ahead of their use; epi(acc, tm, tn)
 // must not touch the stage arrays (its own LDS and barriers are fine).
-template <bool AK, bool BKM, class Coords, class Pre, class Epi>
+// kContiguousRows (K-major A only): A rows are read in the contiguous_row
+// order, so each lane's accumulator elements 0 .. 15 are 16 consecutive rows.
+template <bool AK, bool BKM, bool kContiguousRows = false, class Coords, class Pre, class Epi>
 __device__ __forceinline__ void persistent(Operand A, Operand B, int M, int N, int K, int ntiles, Coords coords,
                                            Pre pre, Epi epi) {
+  static_assert(AK || !kContiguousRows, "row permutation needs a K-major A operand");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int arow = kContiguousRows ? contiguous_row(lane & 31) : (lane & 31);
   int t = blockIdx.x;
   if (t >= ntiles) return;  // uniform
   const int nk = K / BK;
   int tm, tn;
   coords(t, tm, tn);
   Ctx c{make_src<AK>(A, tm * BM, 0, M, K, wave, lane), make_src<BKM>(B, tn * BN, 0, N, K, wave, lane),
-        128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid};
+        128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid, arow};
   fill(stage_ptr<0>(), c, 0);
   fill(stage_ptr<1>(), c, 1);
   fill(stage_ptr<2>(), c, 2);
@@ -292,7 +306,8 @@ __device__ __forceinline__ void persistent(Operand A, Operand B, int M, int N, i
     if (has_next) coords(t_next, tm_n, tn_n);
     // Sources of the next tile; with none, extents of 0 make every copy read zeros.
     const Ctx cn{make_src<AK>(A, tm_n * BM, 0, has_next ? M : 0, K, wave, lane),
-                 make_src<BKM>(B, tn_n * BN, 0, has_next ? N : 0, K, wave, lane), c.wm0, c.wn0, wave, lane, tid};
+                 make_src<BKM>(B, tn_n * BN, 0, has_next ? N : 0, K, wave, lane), c.wm0, c.wn0, wave, lane, tid,
+                 arow};
     step_fill<AK, BKM, 0>(acc, c, cn, 0, a0, b0);
     step_fill<AK, BKM, 1>(acc, c, cn, 1, a0, b0);
     step_fill<AK, BKM, 2>(acc, c, cn, 2, a0, b0);
@@ -481,7 +496,7 @@ __device__ __forceinline__ void mainloop_pp(f32x16 (&acc)[4][2], Operand A, Oper
   // Whole groups of four stages: the stages past the K range read zeros and
   // add nothing, and the loop body stays free of conditions.
   const int nk = (nk_real + 3) & ~3;
-  const Ctx c{Src{}, Src{}, 128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid};
+  const Ctx c{Src{}, Src{}, 128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid, lane & 31};
   int colsum_r = 0;
   Frags f;
   if (g == 0) {
