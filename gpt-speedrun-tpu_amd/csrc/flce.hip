@@ -401,14 +401,20 @@ __global__ void zero_f32_kernel(float* __restrict__ x, int64_t n) {
 
 inline unsigned tiles_of(int M, int N) { return (unsigned)(ceil_div(M, BM) * ceil_div(N, BN)); }
 
-// Default vocabulary chunk of the backward: a third of the vocabulary (rounded
-// up to the 256-row tile), so the G^T workspace stays a third of the logits.
-constexpr int kDefaultChunkParts = 3;
+// Default vocabulary chunk of the backward: the whole vocabulary while the
+// bf16 G^T workspace (n x chunk) fits kGradChunkBudget, else the fewest equal
+// chunks (whole 256-row tiles) that fit.  One chunk measured fastest.
+constexpr size_t kGradChunkBudget = size_t(8) << 30;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int resolve_chunk(int vocab, int vocab_chunk) {
-  int chunk = vocab_chunk <= 0 ? ceil_div(ceil_div(vocab, kDefaultChunkParts), BM) * BM : vocab_chunk;
+int resolve_chunk(int n, int vocab, int vocab_chunk) {
+  int chunk = vocab_chunk;
+  if (chunk <= 0) {
+    const size_t bytes = size_t(2) * (size_t)n * (size_t)vocab;
+    const int parts = (int)((bytes + kGradChunkBudget - 1) / kGradChunkBudget);
+    chunk = ceil_div(ceil_div(vocab, parts < 1 ? 1 : parts), BM) * BM;
+  }
   const int full = ceil_div(vocab, BM) * BM;
   return chunk > full ? full : chunk;
 }
@@ -454,7 +460,7 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
 }
 
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk) {
-  const int chunk = resolve_chunk(vocab, vocab_chunk);
+  const int chunk = resolve_chunk(n, vocab, vocab_chunk);
   return align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16)) + align256((size_t)n * d * sizeof(float));
 }
 
@@ -470,7 +476,7 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
   if (workspace_bytes < gptrig_flce_bwd_workspace_bytes(n, d, vocab, vocab_chunk)) return GPTRIG_E_WORKSPACE;
   if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)workspace | (uintptr_t)dweight) & 15)
     return GPTRIG_E_SHAPE;
-  const int chunk = resolve_chunk(vocab, vocab_chunk);
+  const int chunk = resolve_chunk(n, vocab, vocab_chunk);
   bf16* gt = (bf16*)workspace;
   float* dh_acc = (float*)((char*)workspace + align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16)));
   hipStream_t s = (hipStream_t)stream;

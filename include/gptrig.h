@@ -96,8 +96,9 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
  * scalar `cotangent_scale` for every token (1/n for the mean loss).
  * dhidden: bf16 [n, d].  dweight: f32 [vocab, d]; accumulate_dweight != 0 adds
  * into it (micro-batch accumulation), otherwise it is overwritten.
- * vocab_chunk (multiple of 256, 0 = default) bounds the [n, vocab_chunk]
- * logit-gradient workspace. */
+ * vocab_chunk (multiple of 256) bounds the [n, vocab_chunk] bf16
+ * logit-gradient workspace; 0 = the whole vocabulary while that workspace
+ * fits 8 GiB, else the fewest equal chunks that fit. */
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk);
 int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
                     const float* cotangent, float cotangent_scale, void* dhidden, float* dweight,

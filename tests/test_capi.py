@@ -63,6 +63,24 @@ def test_workspace_queries_are_bounded_by_the_chunk():
     assert small < 16384 * 50304 * 2
 
 
+def test_default_chunk_follows_the_workspace_budget():
+    # vocab_chunk = 0: the whole vocabulary while the bf16 G^T workspace fits
+    # 8 GiB, else the fewest equal 256-row-tile chunks; the same choice as the
+    # Python wrapper's grad_chunk.
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    for n in (16384, 65536, 131072, 262144):
+        vocab = 50304
+        default = _lib.query("gptrig_flce_bwd_workspace_bytes", n, 768, vocab, 0)
+        chunk = lce.grad_chunk(n, vocab)
+        assert default == _lib.query("gptrig_flce_bwd_workspace_bytes", n, 768, vocab, chunk), n
+        parts = -(-(2 * n * vocab) // (8 << 30))
+        assert chunk == max(256, -(-(-(-vocab // parts)) // 256) * 256), n
+        assert 2 * n * chunk <= (8 << 30) or chunk == 256
+    assert lce.grad_chunk(65536, 50304) == 50432  # one chunk at the step's 65536 tokens
+    assert lce.grad_chunk(262144, 50304) == 12800  # 26.4 GB of G^T: four chunks
+
+
 def test_product_does_not_import_the_oracle():
     pkg = os.path.join(os.path.dirname(HEADER), "..", "gpt-speedrun-tpu_amd", "gptrig")
     for root, _, files in os.walk(pkg):
