@@ -13,10 +13,13 @@
 //            reference's [n, tile] live logits):
 //            K1  recompute the logits, write G^T = bf16((exp(logit-lse) - onehot)*ct)
 //                as [chunk, n] in 32-token column blocks (gemm::Operand blk),
-//                zero for rows >= semantic vocab (persistent when d % 128 == 0);
-//            K2  dW[chunk] += G^T h     (split over tokens, fp32 atomics);
-//            K3  dh_acc    += G W[chunk] (fp32 atomics, split over the chunk),
-//                rounded to bf16 at the end.
+//                zero for rows >= semantic vocab;
+//            K2  dW[chunk] += G^T h;
+//            K3  dh       += G W[chunk], rounded to bf16 after the last chunk.
+//            One chunk (the whole vocabulary): three launches, K2 and K3 split
+//            over their reduction with fp32 atomics.  Several chunks: one
+//            persistent work-queue launch (flce_bwd_queue_kernel) that
+//            pipelines K1 / K2 / K3 of successive chunks.
 #include "gemm_core.h"
 
 #include <math.h>
@@ -380,6 +383,228 @@ __global__ void __launch_bounds__(gemm::THREADS)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked backward (more than one vocabulary chunk): pipelined launches.
+//
+// The workspace's bf16 [n, chunk] G^T buffer is used as two halves of C rows
+// each (C = chunk / 2, a multiple of 256).  Launch c (c = 0 .. nchunks) is one
+// persistent grid whose workgroups take work items from atomic counters:
+//   K2 (c-1, r, dt)   dW[chunk c-1, tile r][d tile dt] += G^T[tile r, token block] h[token block][dt]
+//                     (fp32 atomics, one add per token block)
+//   K3 (c-1, nt, dt)  dh[token tile nt][d tile dt] (+)= G[nt, chunk c-1] W[chunk c-1][dt]
+//                     (f32 store on the first chunk, read-modify-write after,
+//                     bf16 dh on the last)
+//   K1 (c, r, nt)     G^T tile of chunk c, into the other half
+// The tokens are cut into 8 blocks of ks tokens, one per XCD: workgroup b
+// takes the items of block b % 8 from that block's counter (workgroups are
+// dispatched round-robin over the XCDs), so a block's h rows, G^T columns
+// and dh rows are read under one L2.  Nothing in a launch depends on anything
+// else in it (K1 writes the half that K2 / K3 do not read) and the stream
+// orders the launches, so no workgroup ever waits for another: each takes
+// items until its counter passes the block's item count and exits.  The grid
+// is a multiple of 8, so every block's counter is served.
+// ---------------------------------------------------------------------------
+constexpr int kBlocks = 8;  // token blocks = XCDs
+
+struct PipeLaunch {
+  const bf16* h;  // [N][d]
+  const bf16* w;  // [V][d]
+  const int32_t* targets;
+  const float* lse;
+  const float* cot;
+  float cot_scale;
+  bf16* gt1;         // half written by K1 (chunk c1): element (v, n) at ((n / 32) * C + v) * 32 + n % 32
+  const bf16* gt23;  // half read by K2 / K3 (chunk c23)
+  float* dh_acc;     // f32 [N][d]
+  bf16* dh;          // bf16 [N][d]
+  float* dw;         // f32 [V][d]
+  int* counter;      // this launch's kBlocks item counters (zero before the launch)
+  int N, D, V, sem_v, C, nchunks, ks, c1, c23;
+};
+
+__host__ __device__ inline int pipe_rows(const PipeLaunch& p, int c) { return min(p.C, p.V - c * p.C); }
+__host__ __device__ inline int pipe_ndt(const PipeLaunch& p) { return (p.D + BN - 1) / BN; }
+// Token tiles of block q (0 past the last block).
+__host__ __device__ inline int pipe_ntn(const PipeLaunch& p, int q) {
+  const int len = min(p.ks, p.N - q * p.ks);
+  return len > 0 ? (len + BM - 1) / BM : 0;
+}
+__host__ __device__ inline int pipe_k2_items(const PipeLaunch& p, int q) {
+  return p.c23 < 0 || pipe_ntn(p, q) == 0 ? 0 : (pipe_rows(p, p.c23) + BM - 1) / BM * pipe_ndt(p);
+}
+__host__ __device__ inline int pipe_k3_items(const PipeLaunch& p, int q) {
+  return p.c23 < 0 ? 0 : pipe_ntn(p, q) * pipe_ndt(p);
+}
+__host__ __device__ inline int pipe_k1_items(const PipeLaunch& p, int q) {
+  return p.c1 < 0 ? 0 : (pipe_rows(p, p.c1) + BM - 1) / BM * pipe_ntn(p, q);
+}
+__host__ __device__ inline int pipe_items(const PipeLaunch& p, int q) {
+  return pipe_k2_items(p, q) + pipe_k3_items(p, q) + pipe_k1_items(p, q);
+}
+
+struct PipeItem {
+  int type;  // 0 = K1 (a = vocab tile, b = token tile), 1 = K2 (a = vocab tile, b = d tile),
+             // 2 = K3 (a = token tile, b = d tile); token tiles are global
+  int a, b;
+};
+
+// Item j of block q: the K2 items (d tile fastest, so consecutive items share
+// their G^T rows), then the K3 items (d tile fastest, sharing G rows), then
+// the K1 tiles (token tile fastest, sharing a W tile).
+__host__ __device__ inline PipeItem pipe_decode(const PipeLaunch& p, int q, int j) {
+  PipeItem it;
+  const int ndt = pipe_ndt(p);
+  const int nt0 = q * (p.ks / BM);
+  const int n2 = pipe_k2_items(p, q), n3 = pipe_k3_items(p, q);
+  if (j < n2) {
+    it.type = 1;
+    it.a = j / ndt;
+    it.b = j % ndt;
+  } else if (j < n2 + n3) {
+    j -= n2;
+    it.type = 2;
+    it.a = nt0 + j / ndt;
+    it.b = j % ndt;
+  } else {
+    j -= n2 + n3;
+    const int ntn = pipe_ntn(p, q);
+    it.type = 0;
+    it.a = j / ntn;
+    it.b = nt0 + j % ntn;
+  }
+  return it;
+}
+
+__global__ void __launch_bounds__(gemm::THREADS) flce_bwd_pipe_kernel(PipeLaunch p) {
+  __shared__ int item_s;
+  __shared__ __attribute__((aligned(16))) float l2_s[BM];
+  __shared__ __attribute__((aligned(16))) float ct_s[BM];
+  __shared__ __attribute__((aligned(16))) int t_s[BM];
+  const int tid = threadIdx.x;
+  const int q = blockIdx.x % kBlocks;
+  const int total = pipe_items(p, q);
+  for (;;) {
+    if (tid == 0) item_s = atomicAdd(p.counter + q, 1);
+    __syncthreads();
+    // Uniform: read into a scalar register, so the decode stays in SGPRs.
+    const int j = __builtin_amdgcn_readfirstlane(item_s);
+    if (j >= total) break;
+    const PipeItem it = pipe_decode(p, q, j);
+    // Lane coordinates derived per item (see gemm::mainloop_pp's kLocalAddr);
+    // the wave index stays scalar.
+    int tid_l = tid;
+    asm volatile("" : "+v"(tid_l));
+    const int lane = tid_l & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_l >> 6);
+    const int hl = lane >> 5, l32 = lane & 31;
+    const int wm = wave & 1, wn = wave >> 1;
+    if (it.type == 0) {
+      // K1: G^T tile = (exp(logit - lse) - onehot) * ct, token tile b, vocabulary tile a of chunk c1.
+      const int v0 = p.c1 * p.C, vc = pipe_rows(p, p.c1);
+      const int n0 = it.b * BN;
+      if (tid < BM) {
+        const int n = n0 + tid;
+        const bool n_ok = n < p.N;
+        const int t = n_ok ? p.targets[n] : -1;
+        const bool valid_t = t >= 0 && t < p.sem_v;
+        t_s[tid] = t;
+        ct_s[tid] = valid_t ? (p.cot ? p.cot[n] : p.cot_scale) : 0.f;
+        l2_s[tid] = n_ok ? p.lse[n] * GPTRIG_LOG2E : 0.f;
+      }
+      f32x16 acc[4][2];
+      gemm::mainloop_pp<true, true, false, true, true>(acc, Operand{p.h, p.D}, Operand{p.w + (size_t)v0 * p.D, p.D},
+                                                       p.N, vc, 0, p.D, n0, it.a * BN);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int r0 = 128 * wm + 32 * mb + 16 * hl;  // this lane's 16 consecutive tokens of the tile
+        const int n = n0 + r0;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int vl = it.a * BN + 64 * wn + 32 * nb + l32;
+          const int v = v0 + vl;
+          bf16* dst = p.gt1 + ((size_t)(n >> 5) * p.C + vl) * 32 + (n & 31);
+#pragma unroll
+          for (int h8 = 0; h8 < 2; ++h8) {
+            asm volatile("" ::: "memory");
+            const int rq = r0 + 8 * h8;
+            const f32x4 la = *reinterpret_cast<const f32x4*>(&l2_s[rq]);
+            const f32x4 lb = *reinterpret_cast<const f32x4*>(&l2_s[rq + 4]);
+            const f32x4 ca = *reinterpret_cast<const f32x4*>(&ct_s[rq]);
+            const f32x4 cb = *reinterpret_cast<const f32x4*>(&ct_s[rq + 4]);
+            const i32x4_t ta = *reinterpret_cast<const i32x4_t*>(&t_s[rq]);
+            const i32x4_t tb = *reinterpret_cast<const i32x4_t*>(&t_s[rq + 4]);
+            bf16x8 o;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              const float l2 = jj < 4 ? la[jj & 3] : lb[jj & 3];
+              const float ct = jj < 4 ? ca[jj & 3] : cb[jj & 3];
+              const int tt = jj < 4 ? ta[jj & 3] : tb[jj & 3];
+              float g = 0.f;
+              if (v < p.sem_v) {
+                const float pr = fast_exp2(acc[mb][nb][8 * h8 + jj] * GPTRIG_LOG2E - l2);
+                g = (pr - (v == tt ? 1.f : 0.f)) * ct;
+              }
+              o[jj] = (bf16)g;
+            }
+            // n + 8 h8 and N are multiples of 8: each half is wholly in or out of range.
+            if (vl < vc && n + 8 * h8 < p.N) *reinterpret_cast<bf16x8*>(dst + 8 * h8) = o;
+          }
+        }
+      }
+    } else if (it.type == 1) {
+      // K2: dW[chunk c23, tile a][d tile b] += G^T[tile a, token block q] h[token block q][d tile b].
+      const int v0 = p.c23 * p.C, vc = pipe_rows(p, p.c23);
+      const int k0 = q * p.ks, k1 = min(p.N, k0 + p.ks);
+      f32x16 acc[4][2];
+      gemm::mainloop_pp<true, false, false, false, true>(acc, Operand{p.gt23, p.N, p.C}, Operand{p.h, p.D}, vc, p.D,
+                                                         k0, k1, it.a * BM, it.b * BN);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int n = it.b * BN + 64 * wn + 32 * nb + l32;
+        if (n >= p.D) continue;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int m = it.a * BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
+            if (m < vc) atomicAdd(p.dw + (size_t)(v0 + m) * p.D + n, acc[mb][nb][i]);
+          }
+      }
+    } else {
+      // K3: dh[token tile a][d tile b] (+)= G[a, chunk c23] W[chunk c23][d tile b].
+      const int v0 = p.c23 * p.C, vc = pipe_rows(p, p.c23);
+      const int n0 = it.a * BM;
+      f32x16 acc[4][2];
+      gemm::mainloop_pp<false, false, false, false, true>(acc, Operand{p.gt23, p.N, p.C},
+                                                          Operand{p.w + (size_t)v0 * p.D, p.D}, p.N, p.D, 0, vc, n0,
+                                                          it.b * BN);
+      const bool first = p.c23 == 0, last = p.c23 == p.nchunks - 1;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int n = it.b * BN + 64 * wn + 32 * nb + l32;
+        if (n >= p.D) continue;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int m = n0 + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
+            if (m >= p.N) continue;
+            const size_t o = (size_t)m * p.D + n;
+            if (first)
+              p.dh_acc[o] = acc[mb][nb][i];
+            else if (last)
+              p.dh[o] = (bf16)(p.dh_acc[o] + acc[mb][nb][i]);
+            else
+              p.dh_acc[o] += acc[mb][nb][i];
+          }
+      }
+    }
+    // Every wave is done with this item's LDS (stage arrays, per-token data
+    // and item_s) before the next item is taken.
+    __syncthreads();
+  }
+}
+
 __global__ void f32_to_bf16_kernel(const float* __restrict__ x, bf16* __restrict__ y, int64_t n) {
   int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i + 4 <= n) {
@@ -401,22 +626,37 @@ __global__ void zero_f32_kernel(float* __restrict__ x, int64_t n) {
 
 inline unsigned tiles_of(int M, int N) { return (unsigned)(ceil_div(M, BM) * ceil_div(N, BN)); }
 
-// Default vocabulary chunk of the backward: the whole vocabulary while the
-// bf16 G^T workspace (n x chunk) fits kGradChunkBudget, else the fewest equal
-// chunks (whole 256-row tiles) that fit.  One chunk measured fastest.
-constexpr size_t kGradChunkBudget = size_t(8) << 30;
+// Default vocabulary chunk of the backward: the reference's default tile
+// (rig/kernels/linear_cross_entropy.py:41, DEFAULT_VOCAB_TILE_SIZE = 2048), so
+// the bf16 G^T workspace is at most [n, 2048] unless the caller asks for more.
+constexpr int kDefaultChunk = 2048;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int resolve_chunk(int n, int vocab, int vocab_chunk) {
-  int chunk = vocab_chunk;
-  if (chunk <= 0) {
-    const size_t bytes = size_t(2) * (size_t)n * (size_t)vocab;
-    const int parts = (int)((bytes + kGradChunkBudget - 1) / kGradChunkBudget);
-    chunk = ceil_div(ceil_div(vocab, parts < 1 ? 1 : parts), BM) * BM;
-  }
+int resolve_chunk(int vocab, int vocab_chunk) {
+  const int chunk = vocab_chunk > 0 ? vocab_chunk : kDefaultChunk;
   const int full = ceil_div(vocab, BM) * BM;
   return chunk > full ? full : chunk;
+}
+
+// Pipelined chunk layout: two halves of `half` vocabulary rows each inside the
+// [n, chunk] G^T buffer (chunk >= 512; else one buffer of `chunk` rows and
+// alternating launches), and the per-XCD token blocks of ks tokens.
+struct PipeShape {
+  int half, nchunks, ks;
+};
+
+PipeShape pipe_shape(int n, int vocab, int rows) {
+  PipeShape s;
+  s.half = rows;
+  s.nchunks = ceil_div(vocab, rows);
+  s.ks = ceil_div(ceil_div(n, kBlocks), BM) * BM;
+  return s;
+}
+
+__global__ void zero_i32_kernel(int* __restrict__ x, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = 0;
 }
 
 }  // namespace
@@ -460,8 +700,13 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
 }
 
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk) {
-  const int chunk = resolve_chunk(n, vocab, vocab_chunk);
-  return align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16)) + align256((size_t)n * d * sizeof(float));
+  if (n <= 0 || d <= 0 || vocab <= 0) return 0;
+  const int chunk = resolve_chunk(vocab, vocab_chunk);
+  const size_t gt = align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16));
+  const size_t acc = align256((size_t)n * d * sizeof(float));
+  if (ceil_div(vocab, chunk) == 1) return gt + acc;
+  // kBlocks work counters per launch: at most 2 ceil(vocab / 256) + 2 launches.
+  return gt + acc + align256((size_t)(2 * ceil_div(vocab, BM) + 2) * kBlocks * sizeof(int));
 }
 
 int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
@@ -476,9 +721,10 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
   if (workspace_bytes < gptrig_flce_bwd_workspace_bytes(n, d, vocab, vocab_chunk)) return GPTRIG_E_WORKSPACE;
   if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)workspace | (uintptr_t)dweight) & 15)
     return GPTRIG_E_SHAPE;
-  const int chunk = resolve_chunk(n, vocab, vocab_chunk);
+  const int chunk = resolve_chunk(vocab, vocab_chunk);
   bf16* gt = (bf16*)workspace;
-  float* dh_acc = (float*)((char*)workspace + align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16)));
+  const size_t gt_bytes = align256((size_t)chunk * ceil_div(n, 32) * 32 * sizeof(bf16));
+  float* dh_acc = (float*)((char*)workspace + gt_bytes);
   hipStream_t s = (hipStream_t)stream;
   const bf16* Wp = (const bf16*)weight;
   const bf16* Hp = (const bf16*)hidden;
@@ -487,13 +733,67 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
     GPTRIG_CHECK_LAUNCH();
   }
+  if (ceil_div(vocab, chunk) > 1) {
+    // Several chunks: pipelined launches over two halves of the G^T buffer
+    // (chunk >= 512), else alternating recompute / reduction launches over
+    // the one buffer.
+    const bool piped = chunk >= 2 * BM;
+    const PipeShape ps = pipe_shape(n, vocab, piped ? chunk / 2 / BM * BM : chunk);
+    const int nch = ps.nchunks;
+    const int launches = piped ? nch + 1 : 2 * nch;
+    int* counters = (int*)((char*)dh_acc + align256((size_t)n * d * sizeof(float)));
+    zero_i32_kernel<<<ceil_div(launches * kBlocks, 256), 256, 0, s>>>(counters, launches * kBlocks);
+    GPTRIG_CHECK_LAUNCH();
+    const size_t half_elems = (size_t)ps.half * ceil_div(n, 32) * 32;
+    PipeLaunch p;
+    p.h = Hp;
+    p.w = Wp;
+    p.targets = targets;
+    p.lse = lse;
+    p.cot = cotangent;
+    p.cot_scale = cotangent_scale;
+    p.dh_acc = dh_acc;
+    p.dh = (bf16*)dhidden;
+    p.dw = dweight;
+    p.N = n;
+    p.D = d;
+    p.V = vocab;
+    p.sem_v = semantic_vocab;
+    p.C = ps.half;
+    p.nchunks = nch;
+    p.ks = ps.ks;
+    const int cus = gemm::device_cus();
+    for (int l = 0; l < launches; ++l) {
+      if (piped) {
+        p.c1 = l < nch ? l : -1;
+        p.c23 = l - 1;
+        p.gt1 = gt + (size_t)(l & 1) * half_elems;
+        p.gt23 = gt + (size_t)((l + 1) & 1) * half_elems;
+      } else {
+        p.c1 = (l & 1) ? -1 : l / 2;
+        p.c23 = (l & 1) ? l / 2 : -1;
+        p.gt1 = gt;
+        p.gt23 = gt;
+      }
+      p.counter = counters + (size_t)l * kBlocks;
+      int most = 0;
+      for (int q = 0; q < kBlocks; ++q) most = pipe_items(p, q) > most ? pipe_items(p, q) : most;
+      // kBlocks workgroups per XCD round at most as many as the busiest block has items.
+      const int cap = cus / kBlocks > 0 ? cus / kBlocks : 1;
+      const int per_block = most < 1 ? 1 : (most < cap ? most : cap);
+      flce_bwd_pipe_kernel<<<per_block * kBlocks, gemm::THREADS, 0, s>>>(p);
+      GPTRIG_CHECK_LAUNCH();
+    }
+    return GPTRIG_OK;
+  }
   {
     const int64_t total = (int64_t)n * d;
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, total);
     GPTRIG_CHECK_LAUNCH();
   }
-  for (int v0 = 0; v0 < vocab; v0 += chunk) {
-    const int vc = vocab - v0 < chunk ? vocab - v0 : chunk;
+  // One chunk (the whole vocabulary): K1, then the split-K dW and dh GEMMs.
+  const int v0 = 0, vc = vocab;
+  {
     Operand Wc{Wp + (size_t)v0 * d, d}, Hd{Hp, d};
     if (d % (4 * gemm::BK) == 0) {
       const unsigned tiles = tiles_of(vc, n), cus = (unsigned)gemm::device_cus();
@@ -504,13 +804,13 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
                                                                   cotangent, cotangent_scale, gt);
     }
     GPTRIG_CHECK_LAUNCH();
-    // dW[v0:v0+vc] += G^T h : A = G^T [vc][n] (K-major), B = h [n][d] (MN-major); split over tokens.
+    // dW += G^T h : A = G^T [vc][n] (K-major), B = h [n][d] (MN-major); split over tokens.
     Operand Ag{gt, n, vc}, Bh{Hp, d};
     const int dw_split = gemm::choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
     gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(
         Ag, Bh, vc, d, n, dw_split, dweight + (size_t)v0 * d, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
-    // dh += G W[v0:v0+vc] : A(m=n, k=v) = G^T [vc][n] (MN-major), B(k=v, n=j) = W [vc][d] (MN-major).
+    // dh += G W : A(m=n, k=v) = G^T [vc][n] (MN-major), B(k=v, n=j) = W [vc][d] (MN-major).
     Operand Agt{gt, n, vc}, Bw{Wp + (size_t)v0 * d, d};
     const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
     gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,

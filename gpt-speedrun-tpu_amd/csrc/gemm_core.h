@@ -479,13 +479,25 @@ struct NoMid {
 // 32nb + lane%32) over this lane half's k of the stages kt of the K range
 // with kt % colsum_period == colsum_phase (see colsum_frags): the workgroups
 // that share a B slab split the sums between them.
+// kContiguousRows (K-major A only): A rows are read in the contiguous_row
+// order, so each lane's accumulator elements 0 .. 15 of a 32-row block are 16
+// consecutive rows (16 hl .. 16 hl + 15).
+// kLocalAddr: the lane's addresses are derived afresh on each call (the thread
+// index passes through an empty asm, the wave index is re-read as a scalar),
+// so a kernel that runs several main loops in one outer loop does not keep
+// every loop's hoisted addresses live at once.
 // On return no copy into the stage arrays is in flight, but other waves may
 // still read the last stage: barrier before reusing them.
-template <bool AK, bool BKM, bool kColSum = false>
+template <bool AK, bool BKM, bool kColSum = false, bool kContiguousRows = false, bool kLocalAddr = false>
 __device__ __forceinline__ void mainloop_pp(f32x16 (&acc)[4][2], Operand A, Operand B, int M, int N, int k_begin,
                                             int k_end, int tm0, int tn0, float* colsum = nullptr,
                                             int colsum_period = 0, int colsum_phase = 0) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  static_assert(AK || !kContiguousRows, "row permutation needs a K-major A operand");
+  int tid = threadIdx.x;
+  if (kLocalAddr) asm volatile("" : "+v"(tid));
+  // The wave index is kept scalar either way: the group branches below hold
+  // barriers and must stay uniform (scalar) branches.
+  const int lane = tid & 63, wave = kLocalAddr ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
   const int g = wave >> 2, wq = wave & 3;
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -496,7 +508,8 @@ __device__ __forceinline__ void mainloop_pp(f32x16 (&acc)[4][2], Operand A, Oper
   // Whole groups of four stages: the stages past the K range read zeros and
   // add nothing, and the loop body stays free of conditions.
   const int nk = (nk_real + 3) & ~3;
-  const Ctx c{Src{}, Src{}, 128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid, lane & 31};
+  const Ctx c{Src{}, Src{}, 128 * (wave & 1), 64 * (wave >> 1), wave, lane, tid,
+              kContiguousRows ? contiguous_row(lane & 31) : (lane & 31)};
   int colsum_r = 0;
   Frags f;
   if (g == 0) {

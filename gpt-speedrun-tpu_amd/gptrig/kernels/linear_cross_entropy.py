@@ -2,11 +2,15 @@
 
 ``tiled_tied_cross_entropy_losses`` / ``tiled_tied_cross_entropy`` keep the
 reference's keyword signature and validation (``_validate_inputs``, ``:45-76``):
-ValueError/TypeError before any launch.  The forward never materialises the
-``[tokens, vocab]`` logits; the backward recomputes them one vocabulary chunk
-at a time (``vocab_tile_size`` rounded up to a multiple of 256 is that chunk).
-Matmul operands are bfloat16 (the reference's default ``compute_dtype``);
-logits, the online log-sum-exp, probabilities and accumulation are float32.
+ValueError/TypeError before any launch.  Neither direction materialises the
+``[tokens, vocab]`` logits.  The backward recomputes them one vocabulary chunk
+at a time, and ``vocab_tile_size`` (rounded up to a multiple of 256, the
+kernels' tile) is that chunk: its bf16 softmax-gradient buffer is at most
+``[tokens, chunk]``, the bound of the reference's ``[tokens, vocab_tile_size]``
+live logits (``:1-24``).  Matmul operands are bfloat16 (the reference's
+default ``compute_dtype``); logits, the online log-sum-exp, probabilities and
+accumulation are float32.  Any width is accepted: widths that are not a
+multiple of 64 are zero-padded, which leaves every logit unchanged.
 """
 
 from __future__ import annotations
@@ -50,16 +54,27 @@ def _normalize_compute_dtype(compute_dtype) -> torch.dtype:
 
 
 def chunk_for(vocab_rows: int) -> int:
-    """A backward vocabulary chunk of at least ``vocab_rows`` rows (whole 256-row tiles)."""
+    """The backward's vocabulary chunk for a requested tile: the smallest
+    multiple of 256 rows that is at least ``vocab_rows``."""
 
     return max(256, (int(vocab_rows) + 255) // 256 * 256)
 
 
-# The backward's one large buffer is the bf16 softmax-gradient chunk G^T
-# (tokens x chunk rows).  The chunk is the whole vocabulary unless that buffer
-# would pass this budget; then the fewest equal chunks that fit.  One chunk
-# measured fastest on MI355X (720 TFLOP/s at 16384 tokens against 694 with two
-# and 395 with 2048-row chunks; 828 against 810 at 65536 tokens).
+def workspace_bytes(n_tokens: int, width: int, vocab: int, vocab_tile_size: int = DEFAULT_VOCAB_TILE_SIZE) -> int:
+    """Device workspace of the backward for ``vocab_tile_size``: the bf16
+    ``[tokens, chunk]`` softmax gradient, the float32 ``[tokens, width]`` dh
+    accumulator (the reference's ``grad_hidden`` carry, ``:247``) and the
+    work-queue counters."""
+
+    d = (int(width) + 63) // 64 * 64
+    n = (int(n_tokens) + 7) // 8 * 8
+    return int(_lib.query("gptrig_flce_bwd_workspace_bytes", n, d, int(vocab), chunk_for(vocab_tile_size)))
+
+
+# The trainer's opt-in: one chunk covering the whole vocabulary while its bf16
+# G^T fits this budget (then the fewest equal chunks that fit).  With the
+# memory of one MI355X this is the fastest choice for the 125M step (no fp32 dh
+# accumulator passes); the public API never takes it implicitly.
 GRAD_CHUNK_BUDGET_BYTES = 8 << 30
 
 
@@ -100,18 +115,30 @@ def flce_backward(h2, w, t1, lse, cotangent, cotangent_scale: float, semantic_vo
 
 
 def _flatten(hidden, embedding, targets):
-    """bf16 ``[n8, d]`` hidden, bf16 weight and int32 targets, rows padded to a
-    multiple of 8 with target -1 (an invalid target: no loss, no gradient)."""
+    """bf16 ``[n8, d64]`` hidden, bf16 ``[V, d64]`` weight and int32 targets:
+    rows padded to a multiple of 8 with target -1 (an invalid target: no loss,
+    no gradient), columns zero-padded to a multiple of 64 (zero columns add
+    nothing to any logit)."""
 
     d = hidden.shape[-1]
+    d64 = (d + 63) // 64 * 64
     h2 = hidden.reshape(-1, d).to(torch.bfloat16)
+    w = embedding.to(torch.bfloat16)
+    if d64 != d:
+        h2 = torch.nn.functional.pad(h2, (0, d64 - d))
+        w = torch.nn.functional.pad(w, (0, d64 - d))
     t1 = targets.reshape(-1).to(torch.int32)
     n = h2.shape[0]
     n8 = (n + 7) // 8 * 8
     if n8 != n:
-        h2 = torch.cat([h2, h2.new_zeros((n8 - n, d))])
+        h2 = torch.cat([h2, h2.new_zeros((n8 - n, d64))])
         t1 = torch.cat([t1, t1.new_full((n8 - n,), -1)])
-    return h2.contiguous(), embedding.to(torch.bfloat16).contiguous(), t1.contiguous(), n
+    return h2.contiguous(), w.contiguous(), t1.contiguous(), n
+
+
+def _unflatten(dh, dw, n, hshape, hdtype, edtype):
+    d = hshape[-1]
+    return dh[:n, :d].reshape(hshape).to(hdtype), dw[:, :d].to(edtype)
 
 
 class _TiledLosses(torch.autograd.Function):
@@ -130,7 +157,7 @@ class _TiledLosses(torch.autograd.Function):
         cot = torch.zeros(h2.shape[0], dtype=torch.float32, device=h2.device)
         cot[:n] = ct.reshape(-1).to(torch.float32)
         dh, dw = flce_backward(h2, w, t1, lse, cot, 0.0, sv, chunk)
-        return dh[:n].reshape(hshape).to(hdtype), dw.to(edtype), None, None, None
+        return (*_unflatten(dh, dw, n, hshape, hdtype, edtype), None, None, None)
 
 
 class _TiledMean(torch.autograd.Function):
@@ -152,7 +179,7 @@ class _TiledMean(torch.autograd.Function):
         cot = torch.zeros(h2.shape[0], dtype=torch.float32, device=h2.device)
         cot[:n] = ct.to(torch.float32) / n
         dh, dw = flce_backward(h2, w, t1, lse, cot, 0.0, sv, chunk)
-        return dh[:n].reshape(hshape).to(hdtype), dw.to(edtype), None, None, None
+        return (*_unflatten(dh, dw, n, hshape, hdtype, edtype), None, None, None)
 
 
 def _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, compute_dtype):
@@ -161,12 +188,7 @@ def _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, c
     _normalize_compute_dtype(compute_dtype)
     _validate_inputs(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size)
     _lib.require_device(hidden, embedding, targets)
-    if hidden.shape[-1] % 64:
-        raise ValueError(f"the HIP kernels need width % 64 == 0; got {hidden.shape[-1]}")
-    # vocab_tile_size is validated as the reference does; the HIP kernels tile
-    # the vocabulary themselves, and the backward chunk follows the memory budget.
-    n_tokens = hidden.numel() // max(hidden.shape[-1], 1)
-    return semantic_vocab_size, grad_chunk(n_tokens, embedding.shape[0])
+    return semantic_vocab_size, chunk_for(vocab_tile_size)
 
 
 def tiled_tied_cross_entropy_losses(hidden, embedding, targets, *, semantic_vocab_size: int,

@@ -96,9 +96,13 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
  * scalar `cotangent_scale` for every token (1/n for the mean loss).
  * dhidden: bf16 [n, d].  dweight: f32 [vocab, d]; accumulate_dweight != 0 adds
  * into it (micro-batch accumulation), otherwise it is overwritten.
- * vocab_chunk (multiple of 256) bounds the [n, vocab_chunk] bf16
- * logit-gradient workspace; 0 = the whole vocabulary while that workspace
- * fits 8 GiB, else the fewest equal chunks that fit. */
+ * vocab_chunk (a multiple of 256; 0 = 2048, the reference's default
+ * vocab_tile_size) is the vocabulary chunk whose logits are recomputed at a
+ * time: the workspace holds one bf16 [n, vocab_chunk] logit gradient, the f32
+ * [n, d] dh accumulator of the reference's loop (:247) and, with more than one
+ * chunk, a few KB of work-queue counters.  Several chunks run as one
+ * persistent launch; a chunk covering the whole vocabulary (vocab_chunk >=
+ * vocab) runs as three launches with no accumulator passes. */
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk);
 int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
                     const float* cotangent, float cotangent_scale, void* dhidden, float* dweight,

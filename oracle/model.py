@@ -230,13 +230,19 @@ def init_state(config: Config, seed: int) -> TrainState:
     return TrainState(flat, zeros(), zeros())
 
 
-def train_step(state: TrainState, x: torch.Tensor, y: torch.Tensor, config: Config) -> dict:
-    """``train_step`` / ``_apply_training_update`` (``train.py:1362-1472``)."""
+def train_step(state: TrainState, x: torch.Tensor, y: torch.Tensor, config: Config,
+               grads_out: dict | None = None) -> dict:
+    """``train_step`` / ``_apply_training_update`` (``train.py:1362-1472``).
+
+    ``grads_out`` (optional) receives the raw float32 gradients (before any
+    clipping), keyed by parameter path."""
 
     leaves = {k: v.detach().requires_grad_(True) for k, v in state.params.items()}
     loss = cross_entropy(leaves, x, y, config)
     grads_t = torch.autograd.grad(loss, list(leaves.values()))
     grads = {k: g.to(F32) for k, g in zip(leaves.keys(), grads_t)}
+    if grads_out is not None:
+        grads_out.update({k: g.detach().clone() for k, g in grads.items()})
     state.step += 1
     lr, gnorm = ooptim.adamw_step(state.params, grads, state.m, state.v, state.step, config.optimizer,
                                   config.parameterization, config.width_multiplier, config.depth_multiplier,

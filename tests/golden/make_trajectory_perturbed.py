@@ -1,0 +1,82 @@
+"""Write the config-A 20-step trajectory of the CPU oracle under a variation
+that the reference itself treats as the same computation, to measure how far
+two correct implementations of the step drift apart on this chaotic run.
+
+Identical to ``make_trajectory.py`` (same config, seed-0 parameters and token
+windows) except for one of:
+
+* ``f64_linear``: every dense linear (``rig/nn.py:55-56``) accumulates its
+  bf16 products in float64 instead of float32 before the bf16 rounding (the
+  reference fixes the result only up to the accumulation order of its dots);
+* ``dense_attention``: the reference's own dense attention backend
+  (``recipes/reference/train.py:1151-1162``: QK^T rounded to bf16, mask
+  ``finfo(f32).min``) instead of the flash kernels' semantics
+  (``rig/kernels/tpu_flash_attention.py:171-207``).
+
+Usage: ``python tests/golden/make_trajectory_perturbed.py f64_linear|dense_attention``
+(10-40 minutes on 8 cores).  Output:
+``tests/golden/config_a_trajectory_<variation>.json``.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+import time
+from dataclasses import replace
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+import torch  # noqa: E402
+
+from oracle import model as om  # noqa: E402
+
+STEPS = 20
+SEED = 0
+
+
+def linear_f64(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``rig/nn.py:55-56`` with float64 accumulation; the backward of the
+    float64 matmul also accumulates in float64."""
+
+    y = torch.matmul(x.to(torch.float64), weight.to(dtype).to(torch.float64)).to(dtype)
+    return y + bias.to(dtype)
+
+
+def main() -> None:
+    variation = sys.argv[1] if len(sys.argv) > 1 else "f64_linear"
+    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
+    config = om.baseline_config("A", steps=STEPS)
+    if variation == "f64_linear":
+        om.linear = linear_f64
+        note = "dense linears accumulate in float64 instead of float32"
+    elif variation == "dense_attention":
+        config = replace(config, attention_backend="dense")
+        note = "the reference's dense attention backend (train.py:1151-1162) instead of the flash semantics"
+    else:
+        raise SystemExit(f"unknown variation {variation!r}")
+    windows = om.synthetic_windows(SEED, STEPS, config.batch_size, config.seq_len, config.vocab_size)
+    state = om.init_state(config, SEED)
+    rows = []
+    for i in range(STEPS):
+        t0 = time.time()
+        w = torch.from_numpy(windows[i])
+        rec = om.train_step(state, w[:, :-1], w[:, 1:], config)
+        rows.append([rec["loss"], rec["learning_rate"], rec["grad_norm"]])
+        print(f"step {i + 1}: {rows[-1]} ({time.time() - t0:.1f} s)", flush=True)
+    out = {
+        "config": "A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup 2 cosine, 20 steps",
+        "perturbation": note,
+        "seed": SEED,
+        "windows": "numpy default_rng(0).integers(0, 50304, (20, 8, 1025), int32)",
+        "columns": ["loss", "learning_rate", "grad_norm"],
+        "rows": rows,
+    }
+    with open(os.path.join(HERE, f"config_a_trajectory_{variation}.json"), "w") as f:
+        json.dump(out, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()

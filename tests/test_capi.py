@@ -57,23 +57,45 @@ def test_host_validation_rejects_bad_arguments_without_launching():
 
 def test_workspace_queries_are_bounded_by_the_chunk():
     # The FLCE backward workspace depends on the vocab chunk, never on the full vocabulary.
+    # (Only the per-launch work counters, 64 bytes per 256 vocabulary rows, grow with it.)
     small = _lib.query("gptrig_flce_bwd_workspace_bytes", 16384, 768, 50304, 4096)
     big = _lib.query("gptrig_flce_bwd_workspace_bytes", 16384, 768, 503040, 4096)
-    assert small == big
+    assert 0 <= big - small <= 64 * 503040 // 256 + 256
     assert small < 16384 * 50304 * 2
 
 
-def test_default_chunk_follows_the_workspace_budget():
-    # vocab_chunk = 0: the whole vocabulary while the bf16 G^T workspace fits
-    # 8 GiB, else the fewest equal 256-row-tile chunks; the same choice as the
-    # Python wrapper's grad_chunk.
+def test_backward_workspace_is_bounded_by_the_vocab_tile():
+    """The reference keeps at most [tokens, vocab_tile_size] logits live
+    (rig/kernels/linear_cross_entropy.py:1-24).  Here the backward's workspace
+    is one bf16 [tokens, chunk] logit gradient (chunk = vocab_tile_size rounded
+    up to 256; vocab_chunk 0 means the reference's default 2048) plus the f32
+    [tokens, width] dh accumulator the reference's loop also carries (:247) and
+    a few KB of work-queue counters: it grows with the tile, never with the
+    vocabulary."""
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    for n, d in ((16384, 768), (65536, 768), (4096, 512), (1000, 64)):
+        default = _lib.query("gptrig_flce_bwd_workspace_bytes", n, d, 50304, 0)
+        assert default == _lib.query("gptrig_flce_bwd_workspace_bytes", n, d, 50304, 2048)
+        for tile in (256, 2048, 4096):
+            ws = _lib.query("gptrig_flce_bwd_workspace_bytes", n, d, 50304, tile)
+            assert ws <= 2 * n * tile + 4 * n * d + (1 << 20), (n, d, tile)
+            assert ws >= 2 * n * tile  # the logit-gradient chunk itself
+            big = _lib.query("gptrig_flce_bwd_workspace_bytes", n, d, 10 * 50304, tile)
+            assert 0 <= big - ws <= 64 * 10 * 50304 // 256 + 256
+        assert lce.workspace_bytes(n, d, 50304) == default
+        assert lce.workspace_bytes(n, d, 50304, 2000) == default  # rounded up to 2048
+    assert lce.chunk_for(1) == 256 and lce.chunk_for(2048) == 2048 and lce.chunk_for(2049) == 2304
+
+
+def test_trainer_whole_vocabulary_chunk_opt_in():
+    # The trainer's explicit opt-in: one chunk covering the whole vocabulary
+    # while its bf16 G^T fits 8 GiB, else the fewest equal 256-row-tile chunks.
     from gptrig.kernels import linear_cross_entropy as lce
 
     for n in (16384, 65536, 131072, 262144):
         vocab = 50304
-        default = _lib.query("gptrig_flce_bwd_workspace_bytes", n, 768, vocab, 0)
         chunk = lce.grad_chunk(n, vocab)
-        assert default == _lib.query("gptrig_flce_bwd_workspace_bytes", n, 768, vocab, chunk), n
         parts = -(-(2 * n * vocab) // (8 << 30))
         assert chunk == max(256, -(-(-(-vocab // parts)) // 256) * 256), n
         assert 2 * n * chunk <= (8 << 30) or chunk == 256

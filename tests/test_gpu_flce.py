@@ -1,0 +1,162 @@
+"""GPU parity of the FLCE backward's two paths, through the C ABI (ctypes).
+
+* the chunked backward (several vocabulary chunks: the public API's default
+  ``vocab_tile_size`` = 2048, pipelined launches over two halves of the
+  ``[tokens, chunk]`` buffer) and the one-chunk launches (the trainer's
+  whole-vocabulary opt-in) against the CPU oracle
+  (``oracle.flce``, restating ``rig/kernels/linear_cross_entropy.py``), at
+  config C's full size (16384 tokens x 768 x 50304) and at small ragged
+  shapes;
+* the reference's width-5 bfloat16 fixture (``tests/test_linear_cross_entropy.py:
+  73-80,129-152``), through the zero-padded public API.
+
+Tolerances: mean loss relative error <= 1e-3 (north star), per-token loss
+``1e-3 |loss| + 2e-4``, dh and dW max-abs <= 2% of their largest magnitude
+(bf16 operands of the reference's own tiled matmuls).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import flce as oflce
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def maxabs(a, b):
+    return float((a.float().cpu() - b.float().cpu()).abs().max())
+
+
+def inputs(n, d, V, sv, seed, h_scale=1.0, w_scale=0.02):
+    g = torch.Generator().manual_seed(seed)
+    h = (torch.randn((n, d), generator=g) * h_scale).to(torch.bfloat16)
+    w = torch.randn((V, d), generator=g) * w_scale
+    t = torch.randint(0, sv, (n,), generator=g, dtype=torch.int32)
+    return h, w, t
+
+
+def run_backward(h, w, t, sv, chunk, ct=None, scale=0.0, dweight=None, accumulate=False):
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    hg, wg, tg = h.to(DEV), w.to(torch.bfloat16).to(DEV), t.to(DEV)
+    losses, lse = lce.flce_forward(hg, wg, tg, sv)
+    dh, dw = lce.flce_backward(hg, wg, tg, lse, None if ct is None else ct.to(DEV), scale, sv, chunk,
+                               dweight=dweight, accumulate=accumulate)
+    torch.cuda.synchronize()
+    return losses.cpu(), lse.cpu(), dh.cpu(), dw.cpu()
+
+
+@pytest.mark.skip(reason="ran the in-kernel work-queue FLCE backward (cross-workgroup dependency counters), which "
+                         "went silent for 180 s on its first GPU run with no cause found by reading; that kernel is "
+                         "removed, and the chunked path (pipelined launches, no waits inside a launch) is covered by "
+                         "test_config_c_pipelined_default_tile_matches_oracle")
+def test_config_c_default_tile_and_whole_vocabulary_match_oracle():
+    """Config C (16384 x 768 x 50304) through the removed work-queue kernel."""
+
+
+def test_config_c_pipelined_default_tile_matches_oracle():
+    """Config C (16384 x 768 x 50304, W ~ N(0, 0.02), mean loss): the public
+    API's default tile (2048: 50 chunks of 1024 rows, 51 pipelined launches)
+    and the trainer's single chunk against the oracle's tiled reference."""
+    import time
+
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    n, d, V = 16384, 768, 50304
+    print(f"flce config C n={n} d={d} V={V}: oracle on the CPU", flush=True)
+    h, w, t = inputs(n, d, V, V, 51)
+    torch.set_num_threads(16)
+    t0 = time.time()
+    losses_ref, lse_ref = oflce.losses_and_lse(h, w, t, semantic_vocab_size=V, vocab_tile_size=2048)
+    print(f"oracle forward {time.time() - t0:.1f} s", flush=True)
+    ct = torch.full((n,), 1.0 / n)
+    dh_ref, dw_ref = oflce.losses_backward(h, w, t, lse_ref, ct, semantic_vocab_size=V, vocab_tile_size=2048)
+    print(f"oracle backward done {time.time() - t0:.1f} s; GPU public API", flush=True)
+    sh, sw = float(dh_ref.float().abs().max()), float(dw_ref.abs().max())
+    # Public API, default vocab_tile_size (2048).
+    hg = h.to(DEV).requires_grad_(True)
+    wg = w.to(DEV).requires_grad_(True)
+    loss = lce.tiled_tied_cross_entropy(hg, wg, t.to(DEV), semantic_vocab_size=V)
+    loss.backward()
+    torch.cuda.synchronize()
+    want = float(losses_ref.mean())
+    print(f"mean loss gpu {float(loss):.6f} oracle {want:.6f}; dh {maxabs(hg.grad, dh_ref) / sh:.4f}, "
+          f"dW {maxabs(wg.grad, dw_ref) / sw:.4f} of max", flush=True)
+    assert abs(float(loss) - want) <= 1e-3 * abs(want)
+    assert maxabs(hg.grad, dh_ref) <= 2e-2 * sh
+    assert maxabs(wg.grad, dw_ref) <= 2e-2 * sw
+    # Trainer opt-in: one chunk, scalar cotangent.
+    print("GPU one chunk", flush=True)
+    _, _, dh1, dw1 = run_backward(h, w, t, V, lce.grad_chunk(n, V), scale=1.0 / n)
+    assert maxabs(dh1, dh_ref) <= 2e-2 * sh
+    assert maxabs(dw1, dw_ref) <= 2e-2 * sw
+    # The two paths sum the same bf16 products in different fp32 orders.
+    assert maxabs(dh1, hg.grad) <= 1e-2 * sh
+
+
+CHUNKED_CASES = [
+    # (n, d, V, semantic V, chunk): ragged token tiles, partial d tiles, ragged last chunks, the
+    # alternating (256-row chunk) and pipelined (>= 512) forms
+    (2056, 192, 1300, 1297, 512),
+    (4096, 768, 5000, 4999, 1024),
+    (8, 64, 600, 600, 256),
+    (1536, 320, 2311, 2000, 768),
+    (296, 128, 1000, 997, 256),
+]
+
+
+@pytest.mark.parametrize("n,d,V,sv,chunk", CHUNKED_CASES)
+def test_chunked_backward_matches_oracle(n, d, V, sv, chunk):
+    print(f"flce chunked case n={n} d={d} V={V} sv={sv} chunk={chunk}", flush=True)
+    h, w, t = inputs(n, d, V, sv, 61, 0.5, 0.5)
+    t[::13] = -1  # invalid targets: no gradient
+    g = torch.Generator().manual_seed(62)
+    ct = torch.rand(n, generator=g)
+    losses_ref, lse_ref = oflce.losses_and_lse(h, w, t, semantic_vocab_size=sv, vocab_tile_size=chunk)
+    dh_ref, dw_ref = oflce.losses_backward(h, w, t, lse_ref, ct, semantic_vocab_size=sv, vocab_tile_size=chunk)
+    losses, lse, dh, dw = run_backward(h, w, t, sv, chunk, ct=ct)
+    finite = torch.isfinite(losses_ref)
+    assert torch.equal(finite, torch.isfinite(losses))
+    assert bool(((losses[finite] - losses_ref[finite]).abs() <= 1e-3 * losses_ref[finite].abs() + 2e-4).all())
+    sh, sw = float(dh_ref.float().abs().max()), float(dw_ref.abs().max())
+    assert maxabs(dh, dh_ref) <= 2e-2 * sh
+    assert maxabs(dw, dw_ref) <= 2e-2 * sw
+    assert (dw[sv:] == 0).all()
+    # accumulate_dweight: adds into an existing dW; the second call sees the same inputs.
+    base = torch.randn(V, d, generator=g)
+    _, _, dh2, dw2 = run_backward(h, w, t, sv, chunk, ct=ct, dweight=base.to(DEV), accumulate=True)
+    assert torch.equal(dh2, dh)
+    assert maxabs(dw2 - base, dw) <= 1e-5 * max(1.0, float(base.abs().max()))
+
+
+def test_width_five_bfloat16_fixture():
+    """tests/test_linear_cross_entropy.py:129-152 of the reference: hidden
+    (2, 3, 5) from default_rng(7) as bfloat16, embedding (13, 5) from
+    default_rng(11), semantic vocabulary 11, tile 7; the value within
+    4e-3 of the dense bf16 oracle, gradients in the input dtypes."""
+    from gptrig.kernels import tiled_tied_cross_entropy
+
+    hidden = torch.from_numpy(np.random.default_rng(7).normal(size=(2, 3, 5)).astype(np.float32)).to(torch.bfloat16)
+    embedding = torch.from_numpy(np.random.default_rng(11).normal(size=(13, 5)).astype(np.float32))
+    targets = torch.tensor([[0, 1, 10], [3, 8, 6]], dtype=torch.int32)
+    hg = hidden.to(DEV).requires_grad_(True)
+    eg = embedding.to(DEV).requires_grad_(True)
+    value = tiled_tied_cross_entropy(hg, eg, targets.to(DEV), semantic_vocab_size=11, vocab_tile_size=7)
+    value.backward()
+    h2 = hidden.clone().requires_grad_(True)
+    e2 = embedding.clone().requires_grad_(True)
+    oracle = oflce.dense_losses(h2, e2, targets, 11, torch.bfloat16).mean()
+    oracle.backward()
+    print(f"width 5: gpu {float(value):.6f} dense {float(oracle):.6f}", flush=True)
+    assert abs(float(value) - float(oracle)) <= 4e-3 + 4e-3 * abs(float(oracle))
+    assert value.dtype == torch.float32
+    assert hg.grad.dtype == torch.bfloat16 and eg.grad.dtype == torch.float32
+    assert tuple(hg.grad.shape) == (2, 3, 5) and tuple(eg.grad.shape) == (13, 5)
+    assert maxabs(hg.grad, h2.grad) <= 2e-2 * float(h2.grad.float().abs().max())
+    assert maxabs(eg.grad, e2.grad) <= 2e-2 * float(e2.grad.abs().max())
+    assert (eg.grad[11:] == 0).all()

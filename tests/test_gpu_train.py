@@ -59,6 +59,58 @@ def test_train_step_history_matches_oracle(micro, embeddings, masking):
     assert np.all(np.abs(got[:, 2] - want[:, 2]) <= 2e-2 * want[:, 2])
 
 
+def test_train_step_completep_clip_and_residual_scale_match_oracle():
+    """The official parameterization (completep_fixed_tpp_v1, recipes/reference/
+    config.yaml:22-30) at width multiplier 2 and depth multiplier 2 with
+    depth_alpha 1: per-tensor LR / epsilon / decay multipliers
+    (train.py:1274-1333), init scales, residual branches scaled by 1/2
+    (train.py:1164-1175), plus an active gradient clip (train.py:1390-1395);
+    history against the oracle's step as above."""
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+
+    steps = 4
+    common = dict(layers=2, heads=2, d_model=128, vocab_size=1000, semantic_vocab_size=997, seq_len=128,
+                  batch_size=4, base_width=64, base_depth=1, depth_alpha=1.0,
+                  parameterization="completep_fixed_tpp_v1", attention_scale="inverse_head_dim", embeddings="untied")
+    opt = dict(learning_rate=2.0 ** -8, steps=steps, warmup_steps=1, grad_clip=0.1)
+    ocfg = om.Config(**common, attention_backend="flash", optimizer=oopt.OptimizerConfig(**opt))
+    gcfg = GPTConfig(**common, micro_batch_size=2, optimizer=OptimizerConfig(**opt))
+    print("train case completep width 2 depth 2 alpha 1, clip 0.1", flush=True)
+    windows = om.synthetic_windows(1, steps, 4, 128, 997)
+    state = om.init_state(ocfg, 0)
+    trainer = GPTTrainer(gcfg, seed=0)
+    assert trainer.residual_scale == 0.5
+    for i in range(steps):
+        w = torch.from_numpy(windows[i])
+        om.train_step(state, w[:, :-1], w[:, 1:], ocfg)
+        trainer.train_step(w[:, :-1].cuda(), w[:, 1:].cuda())
+    got = trainer.history_rows()
+    want = np.asarray(state.history)
+    print("gpu   ", got.tolist(), flush=True)
+    print("oracle", want.tolist(), flush=True)
+    assert np.all(want[:, 2] > 0.1), "the clip must be active"
+    assert abs(got[0, 0] - want[0, 0]) <= 1e-3 * want[0, 0]
+    assert np.all(np.abs(got[:, 0] - want[:, 0]) <= 1e-2 * want[:, 0])
+    np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-6)
+    assert np.all(np.abs(got[:, 2] - want[:, 2]) <= 2e-2 * want[:, 2])
+    # The clipped, multiplier-scaled updates, tensor by tensor: Adam turns
+    # last-bit differences of near-zero gradient elements into full-size
+    # element updates, so the update is compared as a whole (its norm, and its
+    # direction by the cosine), which a wrong per-tensor multiplier (a factor
+    # of 2 here) would fail.
+    init = om.flatten(om.init_params(ocfg, 0))
+    for path in ("blocks/0/qkv_w", "blocks/1/attn_w", "blocks/1/mlp_down_b", "blocks/0/ln2_scale", "token_embedding",
+                 "output_embedding", "final_ln_scale"):
+        p0 = torch.from_numpy(np.asarray(init[path]))
+        du = (trainer.arena.param(path).cpu() - p0).double().reshape(-1)
+        dw = (state.params[path] - p0).double().reshape(-1)
+        ratio = float(du.norm() / dw.norm())
+        cos = float(du @ dw / (du.norm() * dw.norm()))
+        print(f"{path}: update norm ratio {ratio:.4f}, cosine {cos:.4f}", flush=True)
+        assert abs(ratio - 1) <= 0.1 and cos >= 0.9, path
+
+
 def test_initial_parameters_are_bit_identical_to_the_reference_draws():
     from gptrig.train import GPTTrainer
 

@@ -4,18 +4,18 @@ The expected rows are the committed fixture ``tests/golden/config_a_trajectory.j
 written by ``tests/golden/make_trajectory.py`` (the oracle's ``train_step`` on
 the same seed-0 parameters and token windows).
 
-This run (base LR 2^-8 after a 2-step warmup) is chaotic: Adam's normalised
-updates turn last-bit differences of near-zero gradient components into
-full-size parameter differences, and the loss jumps (step 4's gradient norm
-is 12x step 3's).  Three GPU runs of this very test, differing only in the
-order of fp32 atomic additions, differ from each other by up to 1.3% in
-single-step loss and by up to 8x in single-step gradient norm (spikes at
-different steps).  The gates are therefore:
-  * steps 1-5 (before the divergence grows): loss within 0.2% of the oracle,
-    gradient norm within 1% over steps 1-3;
-  * all 20 steps: mean relative loss difference <= 1% and every step <= 2.5%;
-  * learning rate identical (1e-6 relative); median relative gradient-norm
-    difference <= 10%.
+Gates (the north star's "20-step loss trajectory within 1%", on every step):
+  * every step's loss within 1% of the oracle's, steps 1-5 within 0.1%;
+  * learning rate identical (1e-6 relative);
+  * gradient norm within 1% over steps 1-3, median relative difference <= 5%.
+For scale: two exact restatements of the same step that the reference itself
+treats as equivalent (its dense attention backend instead of the flash
+semantics; float64 instead of float32 accumulation in the linears) stay within
+0.21% of this fixture on every step (``tests/golden/config_a_trajectory_*.json``,
+pinned by ``tests/test_golden_fixture.py``), and this GPU path within 0.15%.
+The gradient norm is the noisier figure (Adam turns last-bit gradient
+differences into parameter differences): those variants differ by up to 10%
+on single steps.
 """
 
 from __future__ import annotations
@@ -60,9 +60,10 @@ def test_config_a_twenty_step_trajectory_matches_oracle():
     print("gpu grad norms   ", np.round(got[:, 2], 4).tolist(), flush=True)
     print("oracle grad norms", np.round(want[:, 2], 4).tolist(), flush=True)
     loss_rel = np.abs(got[:, 0] - want[:, 0]) / want[:, 0]
-    assert np.all(loss_rel[:5] <= 2e-3), loss_rel[:5]
-    assert float(loss_rel.mean()) <= 1e-2 and float(loss_rel.max()) <= 2.5e-2, loss_rel
+    print("loss relative differences", np.round(loss_rel, 5).tolist(), flush=True)
+    assert np.all(loss_rel[:5] <= 1e-3), loss_rel[:5]
+    assert float(loss_rel.max()) <= 1e-2, loss_rel
     np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-6)
     rel = np.abs(got[:, 2] - want[:, 2]) / want[:, 2]
     assert np.all(rel[:3] <= 1e-2), rel[:3]
-    assert float(np.median(rel)) <= 1e-1, rel
+    assert float(np.median(rel)) <= 5e-2, rel
