@@ -24,6 +24,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace {
 
 using gemm::BM;
@@ -659,6 +661,35 @@ __global__ void zero_i32_kernel(int* __restrict__ x, int n) {
   if (i < n) x[i] = 0;
 }
 
+// Scratch of gptrig_flce_fwd_noalloc: a file-scope device array, so that
+// entry point allocates nothing.  Each GPU the library runs on holds its own
+// copy, at its own address, until the process ends.  The host never passes
+// the array's name to a kernel (in host code it is only a handle): the device
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current.
+static __device__ __align__(256) unsigned char scratch[GPTRIG_FLCE_FWD_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device (nullptr if the device
+// index is out of range or the runtime call fails).
+void* scratch_ptr() {
+  static std::once_flag once[kMaxDevices];
+  static void* ptr[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(once[dev], [dev] {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) ptr[dev] = p;
+  });
+  return ptr[dev];
+}
+
+// The forward's launches (validated inputs, workspace of at least
+// gptrig_flce_fwd_workspace_bytes), shared by both entry points.
+int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
+                    void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s);
+
 }  // namespace
 
 extern "C" {
@@ -677,10 +708,32 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
   if (semantic_vocab <= 0 || semantic_vocab > vocab) return GPTRIG_E_SHAPE;
   if (workspace_bytes < gptrig_flce_fwd_workspace_bytes(n, d, vocab)) return GPTRIG_E_WORKSPACE;
   if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)workspace) & 15) return GPTRIG_E_SHAPE;
+  return flce_fwd_launch(hidden, weight, targets, losses, lse, workspace, n, d, vocab, semantic_vocab,
+                         (hipStream_t)stream);
+}
+
+int gptrig_flce_fwd_noalloc(const void* hidden, const void* weight, const int32_t* targets, float* losses,
+                            float* lse, int n, int d, int vocab, int semantic_vocab, void* stream) {
+  if (!hidden || !weight || !targets || !losses || !lse) return GPTRIG_E_NULL;
+  if (n <= 0 || d <= 0 || vocab <= 0 || d % 64) return GPTRIG_E_SHAPE;
+  if (semantic_vocab <= 0 || semantic_vocab > vocab) return GPTRIG_E_SHAPE;
+  if (gptrig_flce_fwd_workspace_bytes(n, d, vocab) > (size_t)GPTRIG_FLCE_FWD_NOALLOC_SCRATCH_BYTES)
+    return GPTRIG_E_WORKSPACE;
+  if (((uintptr_t)hidden | (uintptr_t)weight) & 15) return GPTRIG_E_SHAPE;
+  void* ws = scratch_ptr();
+  if (!ws) return GPTRIG_E_LAUNCH;
+  return flce_fwd_launch(hidden, weight, targets, losses, lse, ws, n, d, vocab, semantic_vocab, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
+                    void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s) {
   const int ntiles = ceil_div(vocab, BM);
   float2* partial = (float2*)workspace;
   float* tlogit = (float*)((char*)workspace + align256((size_t)ntiles * n * sizeof(float2)));
-  hipStream_t s = (hipStream_t)stream;
   Operand W{(const bf16*)weight, d}, Hd{(const bf16*)hidden, d};
   if (d % (4 * gemm::BK) == 0) {
     const unsigned tiles = tiles_of(vocab, n), cus = (unsigned)gemm::device_cus();
@@ -698,6 +751,10 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk) {
   if (n <= 0 || d <= 0 || vocab <= 0) return 0;

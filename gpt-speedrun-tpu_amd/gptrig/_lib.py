@@ -31,6 +31,7 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_attn_bwd_rope": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, P, F, P, P, P]),
     "gptrig_flce_fwd_workspace_bytes": (Z, [I, I, I]),
     "gptrig_flce_fwd": (I, [P, P, P, P, P, P, Z, I, I, I, I, P]),
+    "gptrig_flce_fwd_noalloc": (I, [P, P, P, P, P, I, I, I, I, P]),
     "gptrig_flce_bwd_workspace_bytes": (Z, [I, I, I, I]),
     "gptrig_flce_bwd": (I, [P, P, P, P, P, F, P, P, I, P, Z, I, I, I, I, I, P]),
     "gptrig_rmsnorm_fwd": (I, [P, P, P, P, I, I, P]),

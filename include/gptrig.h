@@ -92,6 +92,21 @@ int gptrig_flce_fwd(const void* hidden, const void* weight, const int32_t* targe
                     void* workspace, size_t workspace_bytes, int n, int d, int vocab, int semantic_vocab,
                     void* stream);
 
+/* The forward with no workspace argument and no allocation.  It has no
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch is a fixed file-scope device array of
+ * GPTRIG_FLCE_FWD_NOALLOC_SCRATCH_BYTES (32 MiB) per GPU, held until the
+ * process ends: sizes whose gptrig_flce_fwd_workspace_bytes exceed it return
+ * GPTRIG_E_WORKSPACE (e.g. up to 16384 tokens at vocab 50304).  The first call
+ * on a device looks up that device's copy (with the device current).  Every
+ * call on one GPU shares the array: calls that overlap on one GPU (different
+ * streams, or host threads) race; calls in one stream are ordered.  Results
+ * equal gptrig_flce_fwd's on the same inputs. */
+#define GPTRIG_FLCE_FWD_NOALLOC_SCRATCH_BYTES (32u << 20)
+int gptrig_flce_fwd_noalloc(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
+                            int n, int d, int vocab, int semantic_vocab, void* stream);
+
 /* Backward.  cotangent: f32 [n] per-token loss cotangents, or NULL to use the
  * scalar `cotangent_scale` for every token (1/n for the mean loss).
  * dhidden: bf16 [n, d].  dweight: f32 [vocab, d]; accumulate_dweight != 0 adds
