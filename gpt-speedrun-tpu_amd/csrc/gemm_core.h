@@ -36,6 +36,8 @@
 // of the current one, so LDS latency hides behind the matrix core.
 #pragma once
 
+#include <mutex>
+
 #include "common.h"
 
 namespace gemm {
@@ -593,15 +595,18 @@ __device__ __forceinline__ void split_tile_coords(int pid, int total, int M, int
 
 // ---- host side: launch shaping ----
 
+// Compute units of the current device, looked up once per device (thread-safe:
+// concurrent first calls on one device wait for the one lookup).
 inline int device_cus() {
+  static std::once_flag once[64];
   static int cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
+  std::call_once(once[dev], [dev] {
     int c = 0;
     if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
     cached[dev] = c;
-  }
+  });
   return cached[dev];
 }
 

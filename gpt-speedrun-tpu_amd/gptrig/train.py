@@ -42,6 +42,7 @@ F32 = torch.float32
 CHUNK = 4096
 BLOCK_LEAVES = ("ln1_scale", "qkv_w", "qkv_b", "attn_w", "attn_b",
                 "ln2_scale", "mlp_up_w", "mlp_up_b", "mlp_down_w", "mlp_down_b")
+DENSE_LINEARS = ("qkv_w", "attn_w", "mlp_up_w", "mlp_down_w")
 
 
 @dataclass(frozen=True)
@@ -67,6 +68,16 @@ class GPTConfig:
     vocab_tile_size: int = 2048
     document_masking: bool = False
     document_boundary_token: int = 50256
+    # Routed (MoE) MLPs, recipes/reference_moe/train.py:242-245: 0 = dense.
+    experts: int = 0
+    expert_top_k: int = 2
+    expert_mult: int = 2
+    router_aux_coefficient: float = 0.01
+    # The backward's FLCE vocabulary chunk: True = one chunk over the whole
+    # vocabulary while its bf16 [tokens, vocab] gradient fits 8 GiB (the
+    # fastest choice on one MI355X); False = vocab_tile_size, the reference's
+    # bounded [tokens, tile] working set.
+    flce_whole_vocab: bool = True
     optimizer: OptimizerConfig = field(default_factory=OptimizerConfig)
 
     @property
@@ -92,6 +103,20 @@ class GPTConfig:
             raise ValueError("micro_batch_size must divide batch_size")
         if self.head_dim not in (64, 128) or self.d_model % 64:
             raise ValueError("the HIP step needs head_dim in {64, 128} and d_model % 64 == 0")
+        if self.experts:
+            # reference_moe/train.py:362-371
+            if self.expert_top_k > self.experts:
+                raise ValueError("expert_top_k must not exceed experts")
+            if self.expert_top_k * self.expert_mult != self.mlp_mult:
+                raise ValueError("must satisfy expert_top_k * expert_mult == mlp_mult so active MLP FLOPs match "
+                                 "the dense tier")
+            if self.experts > 16 or self.expert_top_k > 8 or self.d_model * self.experts > 8192:
+                raise ValueError("the HIP router needs experts <= 16, expert_top_k <= 8, d_model * experts <= 8192")
+            if self.micro_batch_size != self.batch_size:
+                # The balance loss is a product of two global-batch means
+                # (reference_moe/train.py:1292-1296); one pass keeps it exact.
+                raise ValueError("a routed model takes the whole batch in one pass: micro_batch_size must equal "
+                                 "batch_size")
 
 
 def init_params(config: GPTConfig, seed: int) -> dict[str, np.ndarray]:
@@ -106,22 +131,32 @@ def init_params(config: GPTConfig, seed: int) -> dict[str, np.ndarray]:
     flat: dict[str, np.ndarray] = {}
     blocks = []
     for _ in range(config.layers):
-        blocks.append({
+        block = {
             "ln1_scale": np.ones((d,), np.float32),
             "qkv_w": normal(rng, (d, 3 * d), hidden_scale),
             "qkv_b": np.zeros((3 * d,), np.float32),
             "attn_w": normal(rng, (d, d), hidden_scale),
             "attn_b": np.zeros((d,), np.float32),
             "ln2_scale": np.ones((d,), np.float32),
-            "mlp_up_w": normal(rng, (d, hidden), hidden_scale),
-            "mlp_up_b": np.zeros((hidden,), np.float32),
-            "mlp_down_w": normal(rng, (hidden, d), hidden_scale),
-            "mlp_down_b": np.zeros((d,), np.float32),
-        })
+        }
+        if config.experts:
+            # reference_moe/train.py:894-944: the router, then the stacked experts.
+            E, eh = config.experts, config.expert_mult * d
+            block["router_w"] = normal(rng, (d, E), hidden_scale)
+            block["expert_up_w"] = normal(rng, (E, d, eh), hidden_scale)
+            block["expert_up_b"] = np.zeros((E, eh), np.float32)
+            block["expert_down_w"] = normal(rng, (E, eh, d), hidden_scale)
+            block["expert_down_b"] = np.zeros((E, d), np.float32)
+        else:
+            block["mlp_up_w"] = normal(rng, (d, hidden), hidden_scale)
+            block["mlp_up_b"] = np.zeros((hidden,), np.float32)
+            block["mlp_down_w"] = normal(rng, (hidden, d), hidden_scale)
+            block["mlp_down_b"] = np.zeros((d,), np.float32)
+        blocks.append(block)
     flat["token_embedding"] = normal(rng, (config.vocab_size, d), config.init_std)
     for i, block in enumerate(blocks):
-        for name in BLOCK_LEAVES:
-            flat[f"blocks/{i}/{name}"] = block[name]
+        for name, value in block.items():
+            flat[f"blocks/{i}/{name}"] = value
     flat["final_ln_scale"] = np.ones((d,), np.float32)
     if config.embeddings == "untied":
         flat["output_embedding"] = normal(rng, (config.vocab_size, d), config.init_std / config.width_multiplier)
@@ -158,7 +193,8 @@ class ParamArena:
         # forward x W as x (W^T)^T 10-20% faster from this layout, while dX = dy W^T
         # is fastest from the original one, so both are kept.
         self.transposed = {k: torch.empty((s[1], s[0]), dtype=BF16, device=device)
-                           for k, s in self.shapes.items() if k.startswith("blocks/") and k.endswith("_w")}
+                           for k, s in self.shapes.items()
+                           if k.startswith("blocks/") and k.rsplit("/", 1)[-1] in DENSE_LINEARS}
         self.refresh_transposed()
 
     def refresh_transposed(self) -> None:
@@ -214,7 +250,10 @@ class GPTTrainer:
         # fp32 order; four times fewer, four times longer split-K launches).
         T = config.batch_size * config.seq_len
         d, f = config.d_model, config.mlp_mult * config.d_model
-        widths = {"qkv": (d, 3 * d), "attn": (d, d), "mlp_up": (d, f), "mlp_down": (f, d)}
+        widths = {"qkv": (d, 3 * d), "attn": (d, d)}
+        if not config.experts:
+            widths.update({"mlp_up": (d, f), "mlp_down": (f, d)})
+        self.linears = tuple(widths)
         self.lin_in = [{k: torch.empty((T, a), dtype=BF16, device=self.device) for k, (a, _) in widths.items()}
                        for _ in range(config.layers)]
         self.lin_dout = [{k: torch.empty((T, b), dtype=BF16, device=self.device) for k, (_, b) in widths.items()}
@@ -225,6 +264,7 @@ class GPTTrainer:
         self.scale = attention_softmax_scale(config.attention_scale, config.head_dim)
         self.residual_scale = config.depth_multiplier ** (-config.depth_alpha)
         self._ws: dict[str, torch.Tensor] = {}
+        self.router_load = None  # [layers, experts] f32 of the last step (routed models)
         self.timers = None  # optional {name: list[(start_event, end_event)]}
 
     # -- helpers -----------------------------------------------------------------
@@ -251,6 +291,85 @@ class GPTTrainer:
                     timers.setdefault(name, []).append((self_inner.s, self_inner.e))
 
         return _Ctx()
+
+    # -- routed MLP (reference_moe/train.py:1230-1307) ---------------------------------
+    def _routed_forward(self, p: str, xn2: torch.Tensor):
+        """The routed MLP of block ``p`` on the normalised rows ``xn2`` [N, d]:
+        fp32 router logits, top-k routing with the stable bucket sort, the two
+        grouped expert GEMMs (bias + GELU, bias) and the gated combine.  Returns
+        the bf16 [N, d] block output and what the backward and the balance loss
+        need."""
+
+        c, A = self.config, self.arena
+        N, d = xn2.shape
+        E, k, eh = c.experts, c.expert_top_k, c.expert_mult * c.d_model
+        R = N * k
+        dev, s = self.device, _lib.stream()
+        logits = torch.empty((N, E), dtype=F32, device=dev)
+        _lib.call("gptrig_moe_router_logits", xn2.data_ptr(), A.param(p + "router_w").data_ptr(), logits.data_ptr(),
+                  N, d, E, s)
+        probs = torch.empty((N, E), dtype=F32, device=dev)
+        chosen = torch.empty((N, k), dtype=torch.int32, device=dev)
+        gate = torch.empty((N, k), dtype=F32, device=dev)
+        counts = torch.empty(E, dtype=torch.int32, device=dev)
+        order = torch.empty(R, dtype=torch.int32, device=dev)
+        rows = torch.empty(R, dtype=torch.int32, device=dev)
+        position = torch.empty(R, dtype=torch.int32, device=dev)
+        _lib.call("gptrig_moe_route", logits.data_ptr(), probs.data_ptr(), chosen.data_ptr(), gate.data_ptr(),
+                  counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), None, 0, N, E, k, s)
+        grouped = torch.empty((R, d), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_gather_rows", xn2.data_ptr(), rows.data_ptr(), grouped.data_ptr(), R, d, s)
+        pre = torch.empty((R, eh), dtype=BF16, device=dev)
+        hidden = torch.empty((R, eh), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_gmm", grouped.data_ptr(), d, A.w(p + "expert_up_w").data_ptr(), 0, counts.data_ptr(),
+                  A.w(p + "expert_up_b").data_ptr(), 1, hidden.data_ptr(), pre.data_ptr(), eh, R, d, eh, E, s)
+        out = torch.empty((R, d), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_gmm", hidden.data_ptr(), eh, A.w(p + "expert_down_w").data_ptr(), 0, counts.data_ptr(),
+                  A.w(p + "expert_down_b").data_ptr(), 0, out.data_ptr(), None, d, R, eh, d, E, s)
+        combined = torch.empty((N, d), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_combine", out.data_ptr(), position.data_ptr(), gate.data_ptr(), combined.data_ptr(), N,
+                  d, k, s)
+        mean_probability = torch.empty(E, dtype=F32, device=dev)
+        load = torch.empty(E, dtype=F32, device=dev)
+        summary = torch.empty(3, dtype=F32, device=dev)
+        _lib.call("gptrig_moe_stats", logits.data_ptr(), probs.data_ptr(), gate.data_ptr(), counts.data_ptr(), N, E,
+                  k, mean_probability.data_ptr(), load.data_ptr(), summary.data_ptr(), s)
+        return combined, (probs, chosen, gate, counts, position, grouped, pre, hidden, out, mean_probability, load)
+
+    def _routed_backward(self, p: str, xn2: torch.Tensor, state, dm: torch.Tensor) -> torch.Tensor:
+        """VJP of the routed MLP of block ``p`` for the block-output gradient
+        ``dm`` [N, d] plus the balance loss's share (coefficient / layers times
+        E * load, the gradient of the mean probability; the load carries none).
+        Expert and router gradients accumulate into the gradient arena; returns
+        the bf16 gradient of ``xn2``."""
+
+        c, A = self.config, self.arena
+        probs, chosen, gate, counts, position, grouped, pre, hidden, out, _, load = state
+        N, d = xn2.shape
+        E, k, eh = c.experts, c.expert_top_k, c.expert_mult * c.d_model
+        R = N * k
+        dev, s = self.device, _lib.stream()
+        dout = torch.empty((R, d), dtype=BF16, device=dev)
+        dgate = torch.empty(R, dtype=F32, device=dev)
+        _lib.call("gptrig_moe_combine_bwd", dm.data_ptr(), out.data_ptr(), position.data_ptr(), gate.data_ptr(),
+                  dout.data_ptr(), dgate.data_ptr(), N, d, k, s)
+        _lib.call("gptrig_moe_gmm_dw", hidden.data_ptr(), eh, dout.data_ptr(), d, counts.data_ptr(),
+                  A.grad(p + "expert_down_w").data_ptr(), A.grad(p + "expert_down_b").data_ptr(), R, eh, d, E, s)
+        dpre = torch.empty((R, eh), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_gmm", dout.data_ptr(), d, A.w(p + "expert_down_w").data_ptr(), 1, counts.data_ptr(),
+                  None, 2, dpre.data_ptr(), pre.data_ptr(), eh, R, d, eh, E, s)
+        _lib.call("gptrig_moe_gmm_dw", grouped.data_ptr(), d, dpre.data_ptr(), eh, counts.data_ptr(),
+                  A.grad(p + "expert_up_w").data_ptr(), A.grad(p + "expert_up_b").data_ptr(), R, d, eh, E, s)
+        dgrouped = torch.empty((R, d), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_gmm", dpre.data_ptr(), eh, A.w(p + "expert_up_w").data_ptr(), 1, counts.data_ptr(),
+                  None, 0, dgrouped.data_ptr(), None, d, R, eh, d, E, s)
+        dxn2 = torch.empty((N, d), dtype=BF16, device=dev)
+        _lib.call("gptrig_moe_gather_bwd", dgrouped.data_ptr(), position.data_ptr(), dxn2.data_ptr(), N, d, k, s)
+        dmp = (load * (c.router_aux_coefficient * E / c.layers)).contiguous()
+        _lib.call("gptrig_moe_router_bwd", xn2.data_ptr(), A.param(p + "router_w").data_ptr(), probs.data_ptr(),
+                  chosen.data_ptr(), gate.data_ptr(), dgate.data_ptr(), dmp.data_ptr(), dxn2.data_ptr(),
+                  A.grad(p + "router_w").data_ptr(), N, d, E, k, s)
+        return dxn2
 
     # -- forward / backward of one micro-batch --------------------------------------
     def _forward(self, tokens: torch.Tensor, micro: int):
@@ -297,18 +416,23 @@ class GPTTrainer:
                           _lib.ptr(seg), o.data_ptr(), lse.data_ptr(), Bm, H, S, D, attn_strides.data_ptr(),
                           self.scale, stream)
             x1, xn2, rstd2 = add_rmsnorm_forward(x, torch.addmm(A.w(p + "attn_b"), o, A.wt(p + "attn_w").t()),
-                                                 self.residual_scale, A.w(p + "ln2_scale"), out=lin_in[i]["mlp_up"])
-            h = torch.addmm(A.w(p + "mlp_up_b"), xn2, A.wt(p + "mlp_up_w").t())
-            g = lin_in[i]["mlp_down"]
-            _lib.call("gptrig_gelu_fwd", h.data_ptr(), g.data_ptr(), h.numel(), stream)
-            down = torch.addmm(A.w(p + "mlp_down_b"), g, A.wt(p + "mlp_down_w").t())
+                                                 self.residual_scale, A.w(p + "ln2_scale"),
+                                                 out=None if c.experts else lin_in[i]["mlp_up"])
+            if c.experts:
+                down, mlp_state = self._routed_forward(p, xn2)
+            else:
+                h = torch.addmm(A.w(p + "mlp_up_b"), xn2, A.wt(p + "mlp_up_w").t())
+                g = lin_in[i]["mlp_down"]
+                _lib.call("gptrig_gelu_fwd", h.data_ptr(), g.data_ptr(), h.numel(), stream)
+                down = torch.addmm(A.w(p + "mlp_down_b"), g, A.wt(p + "mlp_down_w").t())
+                mlp_state = (h, g)
             if i + 1 < c.layers:
                 x2, xn1_next, rstd1_next = add_rmsnorm_forward(x1, down, self.residual_scale,
                                                                A.w(f"blocks/{i + 1}/ln1_scale"),
                                                                out=lin_in[i + 1]["qkv"])
             else:
                 x2, xf, rstdf = add_rmsnorm_forward(x1, down, self.residual_scale, A.w("final_ln_scale"))
-            saved.append((x, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g))
+            saved.append((x, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, mlp_state))
             x = x2
             if i + 1 < c.layers:
                 xn1, rstd1 = xn1_next, rstd1_next
@@ -337,11 +461,19 @@ class GPTTrainer:
                       lse_ce.data_ptr(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size,
                       stream)
         _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
+        if c.experts:
+            # The per-layer expert load of the step (the reference's router row,
+            # reference_moe/train.py:1881-1908), kept on the device.
+            self.router_load = torch.stack([st[-1] for *_, st in saved])
+            if c.router_aux_coefficient:
+                # + coefficient x mean over layers of E * sum(load * P) (:1347-1371, :1557-1558)
+                aux = sum((st[-1] * st[-2]).sum() for *_, st in saved)
+                self.loss.add_(aux * (c.router_aux_coefficient * c.experts / c.layers))
 
         # ---- backward ----
         # One vocabulary chunk while the bf16 G^T fits the budget (6.6 GB at
-        # 65536 tokens x 50304).
-        chunk = lce.grad_chunk(N, c.vocab_size)
+        # 65536 tokens x 50304), unless the config asks for the bounded tile.
+        chunk = lce.grad_chunk(N, c.vocab_size) if c.flce_whole_vocab else lce.chunk_for(c.vocab_tile_size)
         ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
         dxf = torch.empty((N, d), dtype=BF16, device=self.device)
         with self._timed("flce"):
@@ -349,22 +481,28 @@ class GPTTrainer:
                       loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, ws.data_ptr(), ws.numel(),
                       N, d, c.vocab_size, c.semantic_vocab_size, chunk, stream)
         unit = self.residual_scale == 1.0
-        top = lin_dout[c.layers - 1]["mlp_down"] if unit else None
+        top = lin_dout[c.layers - 1]["mlp_down"] if unit and not c.experts else None
         dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True, out=top)
         attn_ws = self._workspace("attn_bwd", _lib.query("gptrig_attn_bwd_workspace_bytes", Bm, H, S, D))
         rope_c, rope_s = rope_tables(S, D, self.device)
         for i in reversed(range(c.layers)):
             p = f"blocks/{i}/"
-            x_in, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, h, g = saved.pop()
+            x_in, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, mlp_state = saved.pop()
             if unit:
-                dm = dx  # already written into this layer's down-projection gradient rows
+                dm = dx  # (dense) already written into this layer's down-projection gradient rows
+            elif c.experts:
+                dm = (dx * self.residual_scale).to(BF16)
             else:
                 dm = lin_dout[i]["mlp_down"]
                 dm.copy_((dx * self.residual_scale).to(BF16))
-            dg = torch.mm(dm, A.w(p + "mlp_down_w").t())
-            dh = lin_dout[i]["mlp_up"]
-            _lib.call("gptrig_gelu_bwd", dg.data_ptr(), h.data_ptr(), dh.data_ptr(), dh.numel(), stream)
-            dxn2 = torch.mm(dh, A.w(p + "mlp_up_w").t())
+            if c.experts:
+                dxn2 = self._routed_backward(p, xn2, mlp_state, dm)
+            else:
+                h, _ = mlp_state
+                dg = torch.mm(dm, A.w(p + "mlp_down_w").t())
+                dh = lin_dout[i]["mlp_up"]
+                _lib.call("gptrig_gelu_bwd", dg.data_ptr(), h.data_ptr(), dh.data_ptr(), dh.numel(), stream)
+                dxn2 = torch.mm(dh, A.w(p + "mlp_up_w").t())
             dx1, _ = rmsnorm_backward(dxn2, x1, A.w(p + "ln2_scale"), rstd2, A.grad(p + "ln2_scale"), True,
                                       dresidual=dx, out=lin_dout[i]["attn"] if unit else None)
             if unit:
@@ -383,7 +521,7 @@ class GPTTrainer:
                           Bm, H, S, D, bwd_strides.data_ptr(), self.scale, rope_c.data_ptr(), rope_s.data_ptr(),
                           stream)
             dxn1 = torch.mm(dqkv, A.w(p + "qkv_w").t())
-            below = lin_dout[i - 1]["mlp_down"] if (unit and i > 0) else None
+            below = lin_dout[i - 1]["mlp_down"] if (unit and i > 0 and not c.experts) else None
             dx, _ = rmsnorm_backward(dxn1, x_in, A.w(p + "ln1_scale"), rstd1, A.grad(p + "ln1_scale"), True,
                                      dresidual=dx1, out=below)
         _lib.call("gptrig_embedding_bwd", tok.data_ptr(), dx.data_ptr(), A.grad("token_embedding").data_ptr(), N, d,
@@ -419,7 +557,7 @@ class GPTTrainer:
         for j in range(n_micro):
             self._forward_backward(x[j * mb:(j + 1) * mb], y[j * mb:(j + 1) * mb], weight, j)
         for i in range(c.layers):
-            for name in ("qkv", "attn", "mlp_up", "mlp_down"):
+            for name in self.linears:
                 self._weight_grad(f"blocks/{i}/{name}", self.lin_in[i][name], self.lin_dout[i][name])
         self.step_count += 1
         step = self.step_count

@@ -19,12 +19,19 @@ import torch
 
 from . import attention as oattn
 from . import flce as oflce
+from . import moe as omoe
 from . import optim as ooptim
 from .nn import F32, apply_rotary, gelu_tanh, linear, normal, rms_norm
 
 BLOCK_LEAVES = (
     "ln1_scale", "qkv_w", "qkv_b", "attn_w", "attn_b",
     "ln2_scale", "mlp_up_w", "mlp_up_b", "mlp_down_w", "mlp_down_b",
+)
+# Routed blocks (recipes/reference_moe/train.py:914-944): the MLP leaves are
+# replaced by the router and the stacked experts.
+MOE_BLOCK_LEAVES = (
+    "ln1_scale", "qkv_w", "qkv_b", "attn_w", "attn_b",
+    "ln2_scale", "router_w", "expert_up_w", "expert_up_b", "expert_down_w", "expert_down_b",
 )
 
 
@@ -53,6 +60,10 @@ class Config:
     vocab_tile_size: int = 2048
     document_masking: bool = False
     document_boundary_token: int = 50256
+    experts: int = 0                   # reference_moe/train.py:242-245
+    expert_top_k: int = 2
+    expert_mult: int = 2
+    router_aux_coefficient: float = 0.01
     optimizer: ooptim.OptimizerConfig = field(default_factory=ooptim.OptimizerConfig)
 
     @property
@@ -116,18 +127,28 @@ def init_params(config: Config, seed: int) -> dict:
                     if config.parameterization == "completep_fixed_tpp_v1" else 0.02)
     blocks = []
     for _ in range(config.layers):
-        blocks.append({
+        block = {
             "ln1_scale": np.ones((d,), np.float32),
             "qkv_w": normal(rng, (d, 3 * d), hidden_scale),
             "qkv_b": np.zeros((3 * d,), np.float32),
             "attn_w": normal(rng, (d, d), hidden_scale),
             "attn_b": np.zeros((d,), np.float32),
             "ln2_scale": np.ones((d,), np.float32),
-            "mlp_up_w": normal(rng, (d, hidden), hidden_scale),
-            "mlp_up_b": np.zeros((hidden,), np.float32),
-            "mlp_down_w": normal(rng, (hidden, d), hidden_scale),
-            "mlp_down_b": np.zeros((d,), np.float32),
-        })
+        }
+        if config.experts:
+            # reference_moe/train.py:894-944: router, then the stacked experts.
+            E, eh = config.experts, config.expert_mult * d
+            block["router_w"] = normal(rng, (d, E), hidden_scale)
+            block["expert_up_w"] = normal(rng, (E, d, eh), hidden_scale)
+            block["expert_up_b"] = np.zeros((E, eh), np.float32)
+            block["expert_down_w"] = normal(rng, (E, eh, d), hidden_scale)
+            block["expert_down_b"] = np.zeros((E, d), np.float32)
+        else:
+            block["mlp_up_w"] = normal(rng, (d, hidden), hidden_scale)
+            block["mlp_up_b"] = np.zeros((hidden,), np.float32)
+            block["mlp_down_w"] = normal(rng, (hidden, d), hidden_scale)
+            block["mlp_down_b"] = np.zeros((d,), np.float32)
+        blocks.append(block)
     result = {
         "token_embedding": normal(rng, (config.vocab_size, d), config.init_std),
         "blocks": blocks,
@@ -145,7 +166,7 @@ def flatten(params: dict) -> dict:
     for key, value in params.items():
         if key == "blocks":
             for i, block in enumerate(value):
-                for name in BLOCK_LEAVES:
+                for name in block:  # the reference's leaf order
                     flat[f"blocks/{i}/{name}"] = block[name]
         else:
             flat[key] = value
@@ -155,6 +176,18 @@ def flatten(params: dict) -> dict:
 def gpt_hidden(p: dict, tokens: torch.Tensor, config: Config) -> torch.Tensor:
     """``gpt_hidden`` (``train.py:1096-1176``) over flat float32 params."""
 
+    return gpt_hidden_and_router(p, tokens, config)[0]
+
+
+def gpt_hidden_and_router(p: dict, tokens: torch.Tensor, config: Config):
+    """``gpt_hidden`` (``train.py:1096-1176``; routed blocks:
+    ``reference_moe/train.py:1374-1491``) over flat float32 params.
+
+    Returns ``(hidden, balance_loss, loads)``: for a routed model the mean over
+    layers of ``load_balance_loss`` and the per-layer ``[layers, experts]``
+    load; ``(hidden, None, None)`` for a dense one.
+    """
+
     dtype = config.dtype
     batch, length = tokens.shape
     hd = config.head_dim
@@ -163,6 +196,7 @@ def gpt_hidden(p: dict, tokens: torch.Tensor, config: Config) -> torch.Tensor:
                 if config.document_masking else None)
     residual_scale = config.depth_multiplier ** (-config.depth_alpha)
     scale = config.softmax_scale
+    balance, loads = [], []
     for i in range(config.layers):
         b = lambda name: p[f"blocks/{i}/{name}"]  # noqa: E731
         residual = x
@@ -186,19 +220,34 @@ def gpt_hidden(p: dict, tokens: torch.Tensor, config: Config) -> torch.Tensor:
         x = residual + (out if residual_scale == 1.0 else (residual_scale * out).to(dtype))
         residual = x
         xn = rms_norm(x, b("ln2_scale"), dtype)
-        h = gelu_tanh(linear(xn, b("mlp_up_w"), b("mlp_up_b"), dtype))
-        out = linear(h, b("mlp_down_w"), b("mlp_down_b"), dtype)
+        if config.experts:
+            out, mean_probability, load, _, _, _ = omoe.routed_mlp_local(
+                xn, b("router_w"), b("expert_up_w"), b("expert_up_b"), b("expert_down_w"), b("expert_down_b"),
+                experts=config.experts, top_k_count=config.expert_top_k, dtype=dtype)
+            balance.append(omoe.load_balance_loss(mean_probability, load))
+            loads.append(load)
+        else:
+            h = gelu_tanh(linear(xn, b("mlp_up_w"), b("mlp_up_b"), dtype))
+            out = linear(h, b("mlp_down_w"), b("mlp_down_b"), dtype)
         x = residual + (out if residual_scale == 1.0 else (residual_scale * out).to(dtype))
-    return rms_norm(x, p["final_ln_scale"], dtype)
+    hidden = rms_norm(x, p["final_ln_scale"], dtype)
+    if not config.experts:
+        return hidden, None, None
+    return hidden, torch.stack(balance).mean(), torch.stack(loads)
 
 
 def cross_entropy(p: dict, x: torch.Tensor, y: torch.Tensor, config: Config) -> torch.Tensor:
-    """``cross_entropy`` (``train.py:1194-1216``), tiled loss backend."""
+    """``cross_entropy`` (``train.py:1194-1216``), tiled loss backend; for a
+    routed model plus ``router_aux_coefficient`` times the layers' mean balance
+    loss (``reference_moe/train.py:1524-1560``)."""
 
-    hidden = gpt_hidden(p, x, config)
+    hidden, balance, _ = gpt_hidden_and_router(p, x, config)
     head = p.get("output_embedding", p["token_embedding"])
-    return oflce.tiled_tied_cross_entropy(hidden, head, y, semantic_vocab_size=config.semantic_vocab_size,
+    loss = oflce.tiled_tied_cross_entropy(hidden, head, y, semantic_vocab_size=config.semantic_vocab_size,
                                           vocab_tile_size=config.vocab_tile_size, compute_dtype=config.dtype)
+    if balance is not None and config.router_aux_coefficient:
+        loss = loss + config.router_aux_coefficient * balance
+    return loss
 
 
 def eval_step(p: dict, x: torch.Tensor, y: torch.Tensor, mask: torch.Tensor,

@@ -70,11 +70,11 @@ def rope64(x: np.ndarray) -> np.ndarray:
     return np.stack((e * c - o * s, e * s + o * c), -1).reshape(x.shape)
 
 
-def close(got: np.ndarray, want: np.ndarray) -> float:
-    """Largest difference in units of the tolerance (2^-6 relative, floor 2^-6 * 0.1):
+def close(got: np.ndarray, want: np.ndarray, floor: float = 0.1) -> float:
+    """Largest difference in units of the tolerance (2^-6 relative, floor 2^-6 * floor):
     a few bf16 ulps of rounding-order slack."""
 
-    tol = 2.0 ** -6 * np.maximum(np.abs(want), 0.1)
+    tol = 2.0 ** -6 * np.maximum(np.abs(want), floor)
     return float(np.max(np.abs(got - want) / tol))
 
 
@@ -347,3 +347,120 @@ def test_completep_adamw_first_steps_by_hand():
             bc1, bc2 = 1 - 0.9 ** 2, 1 - 0.95 ** 2
             w = w - lr2 * lr_m * ((mm / bc1) / (math.sqrt(vv / bc2) + eps) + (0.1 * dec_m * w if decays else 0.0))
             assert abs(float(p[k][j]) - w) <= 1e-6 * max(1.0, abs(w)), (k, j)
+
+
+# --- routed (MoE) blocks: recipes/reference_moe/train.py:1230-1371,1374-1560 ---
+
+E_MOE, MULT = 4, 2
+
+
+def moe_config(**kw) -> om.Config:
+    return config(layers=1, experts=E_MOE, expert_top_k=2, expert_mult=MULT, mlp_mult=2 * MULT, **kw)
+
+
+def moe_params(cfg, gen):
+    p = params(cfg)
+    d, eh = D_MODEL, MULT * D_MODEL
+    p["token_embedding"] = torch.randn(VOCAB, d, generator=gen)
+    p["blocks/0/expert_up_w"] = torch.randn(E_MOE, d, eh, generator=gen) / math.sqrt(d)
+    p["blocks/0/expert_up_b"] = 0.3 * torch.randn(E_MOE, eh, generator=gen)
+    p["blocks/0/expert_down_w"] = torch.randn(E_MOE, eh, d, generator=gen) / math.sqrt(eh)
+    p["blocks/0/expert_down_b"] = 0.1 * torch.randn(E_MOE, d, generator=gen)
+    return p
+
+
+def test_moe_init_leaf_order_and_draws():
+    """init_params (reference_moe/train.py:894-944): the routed block's leaves in
+    the reference's order, router N(0, 0.02), expert biases zero."""
+    cfg = moe_config()
+    flat = om.flatten(om.init_params(cfg, 0))
+    names = [k.split("/")[-1] for k in flat if k.startswith("blocks/0/")]
+    assert tuple(names) == om.MOE_BLOCK_LEAVES
+    assert flat["blocks/0/router_w"].shape == (D_MODEL, E_MOE)
+    assert flat["blocks/0/expert_up_w"].shape == (E_MOE, D_MODEL, MULT * D_MODEL)
+    assert not np.any(flat["blocks/0/expert_up_b"]) and not np.any(flat["blocks/0/expert_down_b"])
+
+
+def test_identical_experts_reduce_to_the_dense_block():
+    """Every expert the same MLP: the renormalised top-k gates sum to one, so
+    the routed block equals a dense block with that MLP (up to the bf16
+    rounding of the gates and of the scatter-add)."""
+    gen = torch.Generator().manual_seed(8)
+    mcfg = moe_config()
+    p = moe_params(mcfg, gen)
+    p["blocks/0/router_w"] = torch.randn(D_MODEL, E_MOE, generator=gen)
+    for name in ("expert_up_w", "expert_up_b", "expert_down_w", "expert_down_b"):
+        p[f"blocks/0/{name}"] = p[f"blocks/0/{name}"][:1].expand_as(p[f"blocks/0/{name}"]).clone()
+    dcfg = config(layers=1, mlp_mult=MULT)
+    dense = {k: v for k, v in p.items() if "expert" not in k and "router" not in k}
+    dense["blocks/0/mlp_up_w"] = p["blocks/0/expert_up_w"][0]
+    dense["blocks/0/mlp_up_b"] = p["blocks/0/expert_up_b"][0]
+    dense["blocks/0/mlp_down_w"] = p["blocks/0/expert_down_w"][0]
+    dense["blocks/0/mlp_down_b"] = p["blocks/0/expert_down_b"][0]
+    x = tokens()
+    got = hidden(p, x, mcfg)
+    want = hidden(dense, x, dcfg)
+    # (floor 1: the gates' bf16 rounding, about 2^-8 of the branch, shows up in
+    # full where the residual and the branch nearly cancel; the outputs are
+    # RMS-normalised, so of order 1.)
+    assert close(got, want, floor=1.0) <= 1.0
+    # mistake: gates taken from the full softmax (not renormalised over the chosen experts)
+    scale = 2.0 / E_MOE
+    half = {k: v.clone() for k, v in dense.items()}
+    half["blocks/0/mlp_down_w"] = half["blocks/0/mlp_down_w"] * scale
+    half["blocks/0/mlp_down_b"] = half["blocks/0/mlp_down_b"] * scale
+    assert close(hidden(half, x, dcfg), want, floor=1.0) > 10
+
+
+def test_zero_router_routes_to_the_first_experts_with_unit_balance_loss():
+    """Zero router weights: every probability is 1/E and top-2 ties go to the
+    lower indices, so each token uses experts 0 and 1 with gates 1/2; the load
+    is (1/2, 1/2, 0, ...), the balance loss E * sum(load * P) is exactly 1,
+    and the block output is the mean of the two experts' MLPs."""
+    gen = torch.Generator().manual_seed(9)
+    cfg = moe_config()
+    p = moe_params(cfg, gen)
+    p["blocks/0/router_w"].zero_()
+    x = tokens()
+    with torch.no_grad():
+        h, balance, loads = om.gpt_hidden_and_router(p, x, cfg)
+    assert float(balance) == 1.0
+    np.testing.assert_array_equal(loads.numpy(), [[0.5, 0.5, 0.0, 0.0]])
+    # The block equals a dense one whose MLP is the two experts side by side
+    # with the down projection halved (the mean of the two experts' outputs).
+    b = lambda n: p[f"blocks/0/{n}"].numpy()  # noqa: E731
+    up = np.concatenate([b("expert_up_w")[0], b("expert_up_w")[1]], axis=1)
+    upb = np.concatenate([b("expert_up_b")[0], b("expert_up_b")[1]])
+    down = np.concatenate([b("expert_down_w")[0], b("expert_down_w")[1]], axis=0) * 0.5
+    downb = 0.5 * (b("expert_down_b")[0] + b("expert_down_b")[1])
+    dcfg = config(layers=1, mlp_mult=2 * MULT)
+    dense = {k: v for k, v in p.items() if "expert" not in k and "router" not in k}
+    dense["blocks/0/mlp_up_w"] = torch.from_numpy(up)
+    dense["blocks/0/mlp_up_b"] = torch.from_numpy(upb)
+    dense["blocks/0/mlp_down_w"] = torch.from_numpy(down)
+    dense["blocks/0/mlp_down_b"] = torch.from_numpy(downb)
+    assert close(h.double().numpy(), hidden(dense, x, dcfg), floor=1.0) <= 1.0
+    # The training objective adds coefficient x balance (reference_moe/train.py:1557-1558).
+    y = tokens(10)
+    with torch.no_grad():
+        ce = om.cross_entropy(p, x, y, om.replace(cfg, router_aux_coefficient=0.0))
+        total = om.cross_entropy(p, x, y, cfg)
+    assert abs(float(total) - float(ce) - 0.01) <= 1e-6
+
+
+def test_balance_loss_router_gradient_closed_form():
+    """d/d router_w of E * sum_e load_e * mean_t softmax(x_t W)_e with the load
+    a constant (counts carry no gradient, reference_moe/train.py:1272,1296):
+    grad[d, k] = E / T * sum_t x_td p_tk (load_k - sum_e load_e p_te)."""
+    gen = torch.Generator().manual_seed(10)
+    T, d = 40, 16
+    xt = torch.randn(T, d, generator=gen)
+    w = (0.5 * torch.randn(d, E_MOE, generator=gen)).requires_grad_(True)
+    logits = xt @ w
+    probs = torch.softmax(logits, -1)
+    _, chosen = om.omoe.top_k(logits.detach(), 2)
+    load = torch.bincount(chosen.reshape(-1).long(), minlength=E_MOE).float() / (T * 2)
+    om.omoe.load_balance_loss(probs.mean(0), load).backward()
+    x64, p64, l64 = xt.double().numpy(), probs.detach().double().numpy(), load.double().numpy()
+    want = E_MOE / T * x64.T @ (p64 * (l64[None, :] - (p64 * l64[None, :]).sum(-1, keepdims=True)))
+    np.testing.assert_allclose(w.grad.double().numpy(), want, rtol=1e-5, atol=1e-7)
