@@ -23,6 +23,7 @@ import json
 import os
 import sys
 import time
+from dataclasses import replace
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "gpt-speedrun-tpu_amd"))
@@ -51,7 +52,8 @@ def parse_args():
                     help="sequences per forward/backward pass (the global batch of 128 is accumulated over 128 / micro-batch passes; 64 measured fastest: at 128 the attention working set outgrows the L2 + MALL)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention (B) and FLCE (C) configs")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="approximate CPU-baseline budget")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the 4x32 micro-batch split and the config-E (MoE) step lines")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="run one 256 MiB calibration copy, one FLCE forward+backward and one attention "
                          "forward+backward at the bench's micro-batch shapes, and exit (the program profiled by "
@@ -80,6 +82,19 @@ def traffic_pass(micro_batch: int) -> None:
     q, k, v, do = (torch.randn(micro_batch, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
     o, lse2 = fa.flash_forward(q, k, v, None, 0.125)
     fa.flash_backward(q, k, v, o, lse2, do, None, 0.125)
+    torch.cuda.synchronize()
+    del q, k, v, do, o, lse2, h, w, t
+    # One full config-D step (every kernel of the product step, for the counter tables).
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+
+    cfg = GPTConfig(layers=12, heads=12, d_model=768, vocab_size=50304, semantic_vocab_size=50304, seq_len=1024,
+                    batch_size=128, micro_batch_size=micro_batch,
+                    optimizer=OptimizerConfig(learning_rate=2.0 ** -8, steps=1000, warmup_steps=100))
+    trainer = GPTTrainer(cfg, seed=0, history_steps=1)
+    rng = np.random.default_rng(2)
+    win = torch.from_numpy(rng.integers(0, cfg.vocab_size, size=(128, 1025), dtype=np.int32)).to(dev)
+    trainer.train_step(win[:, :-1].contiguous(), win[:, 1:].contiguous())
     torch.cuda.synchronize()
     print("traffic pass done", flush=True)
 
@@ -129,14 +144,18 @@ def isolated_configs(reps: int = 20) -> dict:
     h = torch.from_numpy(rng.standard_normal((n, d), dtype=np.float32)).to(dev).bfloat16()
     w = torch.from_numpy(rng.standard_normal((vocab, d), dtype=np.float32) * 0.02).to(dev).bfloat16()
     t = torch.from_numpy(rng.integers(0, vocab, size=n, dtype=np.int32)).to(dev)
-    chunk = lce.grad_chunk(n, vocab)
+    def flce_with(chunk):
+        def run():
+            _, lse_c = lce.flce_forward(h, w, t, vocab)
+            lce.flce_backward(h, w, t, lse_c, None, 1.0 / n, vocab, chunk)
+        return run
 
-    def flce():
-        _, lse_c = lce.flce_forward(h, w, t, vocab)
-        lce.flce_backward(h, w, t, lse_c, None, 1.0 / n, vocab, chunk)
-
-    flce_ms = timed(flce)
+    # The trainer's whole-vocabulary chunk, and the public API's default
+    # vocab_tile_size (2048: the reference's bounded [tokens, tile] working set).
+    flce_ms = timed(flce_with(lce.grad_chunk(n, vocab)))
     flce_tf = flce_flops(n, d, vocab) / (flce_ms / 1e3) / 1e12
+    tile_ms = timed(flce_with(lce.chunk_for(lce.DEFAULT_VOCAB_TILE_SIZE)))
+    tile_tf = flce_flops(n, d, vocab) / (tile_ms / 1e3) / 1e12
     peak = MFMA_BF16_PEAK_TFLOPS
     return {
         "attention_B16_H12_S1024_D64": {
@@ -144,7 +163,11 @@ def isolated_configs(reps: int = 20) -> dict:
             "bwd_ms": round(bwd_ms, 4), "bwd_tflops": round(bwd_tf, 1), "bwd_frac": round(bwd_tf / peak, 4),
             "bwd_algorithmic_flops": attn_bwd_flops(B, H, S, D)},
         "flce_N16384_d768_V50304": {"ms": round(flce_ms, 4), "tflops": round(flce_tf, 1),
-                                    "frac": round(flce_tf / peak, 4), "algorithmic_flops": flce_flops(n, d, vocab)},
+                                    "frac": round(flce_tf / peak, 4), "algorithmic_flops": flce_flops(n, d, vocab),
+                                    "chunk": "whole vocabulary (the trainer's opt-in)",
+                                    "default_tile_2048": {"ms": round(tile_ms, 4), "tflops": round(tile_tf, 1),
+                                                          "frac": round(tile_tf / peak, 4),
+                                                          "workspace_bytes": lce.workspace_bytes(n, d, vocab)}},
     }
 
 
@@ -167,30 +190,82 @@ def step_flops(layers, d, seq, tokens, vocab, mlp=4):
     return 3 * (per_token + attn) * tokens
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """Time the oracle (CPU restatement) on config D with a bounded batch:
-    forward+backward of ``b`` sequences and one AdamW update over all params,
-    extrapolated to the 128-sequence global batch."""
+def cpu_baseline() -> dict:
+    """The CPU restatement of the reference's semantics (``oracle/``, torch-CPU
+    fp32 math with bf16 rounding at the reference's cast points) on the host
+    cores of this box, as planned in BASELINE.md: config A's full train step
+    (forward, backward, AdamW; median of 5 after 2 warm-ups), the isolated
+    attention (B) and FLCE (C) configs (one timed call after a warm-up), and a
+    config-D figure extrapolated from a measured per-sequence forward+backward
+    (median of 3 after 1 warm-up) plus one AdamW update."""
 
+    import statistics
+
+    from oracle import attention as oattn
+    from oracle import flce as oflce
     from oracle import model as om
     from oracle import optim as oopt
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    cfg = om.baseline_config("D", steps=1000)
-    state = om.init_state(cfg, 0)
-    win = om.synthetic_windows(2, 1, 1, cfg.seq_len, cfg.vocab_size)[0]
-    x, y = torch.from_numpy(win[:, :-1]), torch.from_numpy(win[:, 1:])
+
+    def clock(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    # Config A: the full step, medians of 5 after 2 warm-ups.
+    cfg_a = om.baseline_config("A", steps=1000)
+    state = om.init_state(cfg_a, 0)
+    win = om.synthetic_windows(0, 7, cfg_a.batch_size, cfg_a.seq_len, cfg_a.vocab_size)
+    times = []
+    for i in range(7):
+        w = torch.from_numpy(win[i])
+        t = clock(lambda: om.train_step(state, w[:, :-1], w[:, 1:], cfg_a))
+        if i >= 2:
+            times.append(t)
+    a_step = statistics.median(times)
+    del state
+    # Config B: attention fwd + bwd at B16 H12 S1024 D64 (scale 1/8).
+    g = torch.Generator().manual_seed(1)
+    q, k, v, do = (torch.randn(16, 12, 1024, 64, generator=g).to(torch.bfloat16) for _ in range(4))
+
+    def attn():
+        o, lse = oattn.attention_forward(q, k, v, softmax_scale=0.125)
+        oattn.attention_backward(q, k, v, o, lse, do, softmax_scale=0.125)
+
+    attn()
+    b_s = clock(attn)
+    del q, k, v, do
+    # Config C: FLCE fwd + bwd at N16384 d768 V50304 (tile 2048).
+    hc = torch.randn(16384, 768, generator=g).to(torch.bfloat16)
+    wc = torch.randn(50304, 768, generator=g) * 0.02
+    tc = torch.randint(0, 50304, (16384,), generator=g, dtype=torch.int32)
+    ct = torch.full((16384,), 1.0 / 16384)
+
+    def flce():
+        _, lse = oflce.losses_and_lse(hc, wc, tc, semantic_vocab_size=50304)
+        oflce.losses_backward(hc, wc, tc, lse, ct, semantic_vocab_size=50304)
+
+    flce()
+    c_s = clock(flce)
+    del hc, wc, tc
+    # Config D: per-sequence forward + backward and one AdamW update, extrapolated.
+    cfg_d = om.baseline_config("D", steps=1000)
+    state = om.init_state(cfg_d, 0)
+    wd = om.synthetic_windows(2, 1, 1, cfg_d.seq_len, cfg_d.vocab_size)[0]
+    x, y = torch.from_numpy(wd[:, :-1]), torch.from_numpy(wd[:, 1:])
     leaves = {k: v.detach().requires_grad_(True) for k, v in state.params.items()}
-    t0 = time.perf_counter()
-    loss = om.cross_entropy(leaves, x, y, cfg)
-    grads = torch.autograd.grad(loss, list(leaves.values()))
-    t_fb = time.perf_counter() - t0
-    g = {k: gr.float() for k, gr in zip(leaves.keys(), grads)}
-    t0 = time.perf_counter()
-    oopt.adamw_step(state.params, g, state.m, state.v, 1, cfg.optimizer)
-    t_adam = time.perf_counter() - t0
-    step_s = 128 * t_fb + t_adam
+
+    def fwd_bwd():
+        loss = om.cross_entropy(leaves, x, y, cfg_d)
+        return torch.autograd.grad(loss, list(leaves.values()))
+
+    grads = fwd_bwd()
+    t_fb = statistics.median(clock(fwd_bwd) for _ in range(3))
+    gd = {k: gr.float() for k, gr in zip(leaves.keys(), grads)}
+    t_adam = clock(lambda: oopt.adamw_step(state.params, gd, state.m, state.v, 1, cfg_d.optimizer))
+    d_step = 128 * t_fb + t_adam
     cpu = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -198,14 +273,61 @@ def cpu_baseline(seconds: float) -> dict:
     except (OSError, StopIteration):
         pass
     return {
-        "value": round(128 * 1024 / step_s, 1),
+        "value": round(128 * 1024 / d_step, 1),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU restatement of reference semantics (oracle/, torch-CPU fp32 math with bf16 rounding) on "
-                   f"config D: fwd+bwd of 1 sequence x 1024 tokens ({t_fb:.2f} s) and one AdamW update over "
-                   f"162.3M params ({t_adam:.2f} s), extrapolated to 128 sequences + 1 update; {cpu}"),
+        "extrapolated": True,
+        "sample": (f"CPU restatement of reference semantics (oracle/, torch-CPU fp32 math with bf16 rounding), "
+                   f"{threads} threads on {cpu}.  value: config D (125M) tokens/s EXTRAPOLATED from a measured "
+                   f"per-sequence forward+backward ({t_fb:.2f} s, median of 3 after a warm-up) x 128 sequences "
+                   f"+ one AdamW update ({t_adam:.2f} s)"),
+        "config_A_step": {"tokens_per_s": round(cfg_a.batch_size * cfg_a.seq_len / a_step, 1),
+                          "s_per_step": round(a_step, 3), "measured": "median of 5 full steps after 2 warm-ups"},
+        "config_B_attention_fwd_bwd_s": round(b_s, 3),
+        "config_C_flce_fwd_bwd_s": round(c_s, 3),
     }
+
+
+def timed_steps(trainer, xs, ys, warmup: int, steps: int) -> float:
+    """ms per step of ``trainer`` over ``steps`` steps after ``warmup`` (device
+    clock, bracketed by synchronisations)."""
+
+    for i in range(warmup):
+        trainer.train_step(xs[i % len(xs)], ys[i % len(ys)])
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        trainer.train_step(xs[(warmup + i) % len(xs)], ys[(warmup + i) % len(ys)])
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def moe_step(expert_mult: int, warmup: int = 2, steps: int = 3) -> dict:
+    """Config E: the MoE recipe's train step (12x768 backbone, 8 experts top-2,
+    seq 1024, batch 32 in one pass, synthetic tokens from numpy seed 2)."""
+
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+
+    cfg = GPTConfig(layers=12, heads=12, d_model=768, vocab_size=50304, semantic_vocab_size=50304, seq_len=1024,
+                    batch_size=32, micro_batch_size=32, experts=8, expert_top_k=2, expert_mult=expert_mult,
+                    mlp_mult=2 * expert_mult, optimizer=OptimizerConfig(learning_rate=2.0 ** -8, steps=1000,
+                                                                        warmup_steps=100))
+    trainer = GPTTrainer(cfg, seed=0, history_steps=warmup + steps)
+    rng = np.random.default_rng(2)
+    win = torch.from_numpy(rng.integers(0, cfg.vocab_size, size=(warmup + steps, 32, 1025), dtype=np.int32)).cuda()
+    xs = [win[i, :, :-1].contiguous() for i in range(warmup + steps)]
+    ys = [win[i, :, 1:].contiguous() for i in range(warmup + steps)]
+    ms = timed_steps(trainer, xs, ys, warmup, steps)
+    tokens = cfg.batch_size * cfg.seq_len
+    loss = float(trainer.history_rows()[-1, 0])
+    del trainer, win, xs, ys
+    torch.cuda.empty_cache()
+    return {"expert_width": expert_mult * 768, "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(tokens / (ms / 1e3), 1), "last_loss": round(loss, 4)}
 
 
 def main():
@@ -304,12 +426,26 @@ def main():
         "adamw": {"ms": round(adam_ms, 3), "achieved_GBps": round(adam_gbs, 1), "peak_GBps": 8000},
         "loss_first_last": [float(hist[0, 0]), float(hist[-1, 0])],
     }
-    del trainer, windows, xs, ys
+    del trainer
     torch.cuda.empty_cache()
+    if not args.no_extra and args.micro_batch != 32:
+        # BASELINE.json's split of the same step: 4 micro-batches of 32.
+        split = GPTTrainer(replace(cfg, micro_batch_size=32), seed=0, history_steps=7)
+        ms = timed_steps(split, xs, ys, 2, 5)
+        result["split_4x32"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tokens_per_step / (ms / 1e3), 1),
+                                "steps": 5, "warmup": 2}
+        del split
+        torch.cuda.empty_cache()
+    del windows, xs, ys
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        result["config_E_moe_step"] = {"workload": "MoE recipe train step: 12x768 backbone, 8 experts top-2, "
+                                                   "seq 1024, batch 32 (one pass), AdamW",
+                                       "reference_valid_width": moe_step(2), "baseline_width": moe_step(4)}
     if not args.no_isolated:
         result["isolated"] = isolated_configs()
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
 
 
