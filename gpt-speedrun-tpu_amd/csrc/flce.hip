@@ -250,8 +250,13 @@ __global__ void __launch_bounds__(gemm::THREADS)
 // runs of 4 tokens and needed four 8-byte stores (measured 0.7% slower for the
 // FLCE backward).  Per-token lse / cotangent / target are staged in
 // LDS, double-buffered by tile parity and loaded a tile ahead.  Tiles are
-// walked one vocabulary tile per token sweep (measured 0.7% faster for the
-// FLCE backward than two per sweep, 0.8% faster than four or eight).
+// walked four vocabulary tiles per token sweep: the 32 workgroups of an XCD
+// then share 4 W slabs and 8 h slabs per round, which cuts this launch's HBM
+// fetch at N = 65536 from 19.7 GB (one vocabulary tile per sweep: 32 h slabs
+// per round, h re-read from HBM for every vocabulary tile) to 7.3 GB, at the
+// same time (13.52 vs 13.51 ms for the whole FLCE backward; eight per sweep
+// fetches 7.4 GB and takes 13.61 ms).  The launch is bound by its MFMA
+// mainloop and softmax epilogue, not by HBM.
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(gemm::THREADS)
     flce_grad_persistent_kernel(Operand W, Operand Hd, int Vc, int N, int D, int v0, int sem_v,
@@ -267,7 +272,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
   int pre_it = 0, epi_it = 0;
   auto coords = [&](int t, int& tm, int& tn) {
     int tv, tt;
-    gemm::tile_coords(t, Vc, N, tv, tt, 1);
+    gemm::tile_coords(t, Vc, N, tv, tt, 4);
     tm = tt;  // token tile
     tn = tv;  // vocabulary tile
   };
