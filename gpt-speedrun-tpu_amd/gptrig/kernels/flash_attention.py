@@ -26,22 +26,25 @@ _KERNEL_DIMS = (64, 128)
 
 @dataclass(frozen=True)
 class AttentionTiles:
-    """Tile plan of the HIP kernels (compile-time; reported, not tuned).
+    """Tile plan of the HIP kernels.
 
-    Field names follow the reference's ``AttentionTilePlan``
-    (``rig/kernels/autotune.py:84-157``).
+    The tiles are fixed at compile time per head dim, so a plan describes
+    the kernels rather than choosing among them (``kernel_tiles``).  Field
+    names follow the reference's ``AttentionTilePlan``
+    (``rig/kernels/autotune.py:84-157``); ``*_compute`` is the sub-tile one
+    wave (one MFMA row block) handles.  The defaults are the head_dim 64 plan.
     """
 
-    block_q: int = 128
-    block_kv: int = 64
-    block_kv_compute: int = 64
-    block_q_dkv: int = 64
+    block_q: int = 128  # forward: queries per workgroup (4 waves x 32)
+    block_kv: int = 64  # forward: keys per LDS tile
+    block_kv_compute: int = 32  # forward: keys per online-softmax half-step
+    block_q_dkv: int = 64  # backward: queries per step
     block_q_dkv_compute: int = 32
-    block_kv_dkv: int = 128
+    block_kv_dkv: int = 256  # backward: keys per workgroup (8 waves x 32)
     block_kv_dkv_compute: int = 32
-    block_q_dq: int = 64
-    block_kv_dq: int = 128
-    block_kv_dq_compute: int = 128
+    block_q_dq: int = 64  # dQ is accumulated by the same (key-owned) workgroups
+    block_kv_dq: int = 256
+    block_kv_dq_compute: int = 32
 
     @property
     def has_backward_tiles(self) -> bool:
@@ -51,14 +54,25 @@ class AttentionTiles:
         return dict(self.__dict__)
 
 
-def attention_tile_candidates(*, sequence: int, head_dim: int, training: bool = True) -> tuple[AttentionTiles, ...]:
-    """The HIP kernels have one tile plan per head dim."""
+def kernel_tiles(head_dim: int) -> AttentionTiles:
+    """The plan the kernels run for ``head_dim`` (padded up to 64 or 128):
+    the head_dim 128 backward owns 128 keys per workgroup (4 waves x 32)."""
 
-    return (AttentionTiles(),)
+    if head_dim <= 0 or head_dim > _KERNEL_DIMS[-1]:
+        raise ValueError(f"head_dim must be in (0, {_KERNEL_DIMS[-1]}]; got {head_dim}")
+    if head_dim <= 64:
+        return AttentionTiles()
+    return AttentionTiles(block_kv_dkv=128, block_kv_dq=128)
+
+
+def attention_tile_candidates(*, sequence: int, head_dim: int, training: bool = True) -> tuple[AttentionTiles, ...]:
+    """The candidate list has one entry: the kernels' fixed plan."""
+
+    return (kernel_tiles(head_dim),)
 
 
 def select_attention_tiles(*, sequence: int, head_dim: int, training: bool = True) -> AttentionTiles:
-    return AttentionTiles()
+    return kernel_tiles(head_dim)
 
 
 @dataclass(frozen=True)
@@ -168,6 +182,9 @@ def make_causal_attention(config: AttentionConfig = AttentionConfig()) -> Callab
 
     def attention(q, k, v, segment_ids=None):
         validate_qkv(q, k, v)
+        if config.tiles is not None and config.tiles != kernel_tiles(q.shape[-1]):
+            raise ValueError(f"the HIP kernels run one fixed tile plan per head dim "
+                             f"({kernel_tiles(q.shape[-1])}); got {config.tiles}")
         scale = float(q.shape[-1] ** -0.5 if config.softmax_scale is None else config.softmax_scale)
         if q.dtype != torch.bfloat16:
             raise TypeError(f"the HIP flash kernel supports bfloat16 q/k/v; got {q.dtype}")

@@ -110,3 +110,22 @@ def test_product_does_not_import_the_oracle():
             if f.endswith(".py"):
                 text = open(os.path.join(root, f)).read()
                 assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), f
+
+
+def test_attention_tile_plan_describes_the_kernels():
+    """The tile-plan API (rig/kernels/autotune.py:84-157) reports the
+    kernels' fixed plan per head dim and rejects any other plan before a
+    launch (CPU tensors: the check runs ahead of the device checks)."""
+    import torch
+
+    from gptrig.kernels import AttentionConfig, AttentionTiles, make_causal_attention, select_attention_tiles
+    from gptrig.kernels.flash_attention import kernel_tiles
+
+    assert select_attention_tiles(sequence=1024, head_dim=64) == AttentionTiles()
+    assert kernel_tiles(64).block_kv_dkv == 256 and kernel_tiles(128).block_kv_dkv == 128
+    assert kernel_tiles(48) == kernel_tiles(64) and kernel_tiles(96) == kernel_tiles(128)
+    q = torch.zeros((1, 2, 16, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="fixed tile plan"):
+        make_causal_attention(AttentionConfig(tiles=AttentionTiles(block_q=64)))(q, q, q)
+    with pytest.raises(ValueError, match="fixed tile plan"):
+        make_causal_attention(AttentionConfig(tiles=kernel_tiles(128)))(q, q, q)
