@@ -399,8 +399,8 @@ __global__ void __launch_bounds__(gemm::THREADS)
 //   K2 (c-1, r, dt)   dW[chunk c-1, tile r][d tile dt] += G^T[tile r, token block] h[token block][dt]
 //                     (fp32 atomics, one add per token block)
 //   K3 (c-1, nt, dt)  dh[token tile nt][d tile dt] (+)= G[nt, chunk c-1] W[chunk c-1][dt]
-//                     (f32 store on the first chunk, read-modify-write after,
-//                     bf16 dh on the last)
+//                     (f32 store on the first chunk, no-return f32 atomics
+//                     after; one conversion to bf16 after the last launch)
 //   K1 (c, r, nt)     G^T tile of chunk c, into the other half
 // The tokens are cut into 8 blocks of ks tokens, one per XCD: workgroup b
 // takes the items of block b % 8 from that block's counter (workgroups are
@@ -423,7 +423,6 @@ struct PipeLaunch {
   bf16* gt1;         // half written by K1 (chunk c1): element (v, n) at ((n / 32) * C + v) * 32 + n % 32
   const bf16* gt23;  // half read by K2 / K3 (chunk c23)
   float* dh_acc;     // f32 [N][d]
-  bf16* dh;          // bf16 [N][d]
   float* dw;         // f32 [V][d]
   int* counter;      // this launch's kBlocks item counters (zero before the launch)
   int N, D, V, sem_v, C, nchunks, ks, c1, c23;
@@ -585,7 +584,11 @@ __global__ void __launch_bounds__(gemm::THREADS) flce_bwd_pipe_kernel(PipeLaunch
       gemm::mainloop_pp<false, false, false, false, true>(acc, Operand{p.gt23, p.N, p.C},
                                                           Operand{p.w + (size_t)v0 * p.D, p.D}, p.N, p.D, 0, vc, n0,
                                                           it.b * BN);
-      const bool first = p.c23 == 0, last = p.c23 == p.nchunks - 1;
+      // The first chunk stores; later chunks add with no-return atomics (the
+      // items of one launch write disjoint tiles and the stream orders the
+      // launches, so these adds never race: the atomic form only avoids a
+      // load round trip per element).  dh is converted after the last launch.
+      const bool first = p.c23 == 0;
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const int n = it.b * BN + 64 * wn + 32 * nb + l32;
@@ -599,10 +602,8 @@ __global__ void __launch_bounds__(gemm::THREADS) flce_bwd_pipe_kernel(PipeLaunch
             const size_t o = (size_t)m * p.D + n;
             if (first)
               p.dh_acc[o] = acc[mb][nb][i];
-            else if (last)
-              p.dh[o] = (bf16)(p.dh_acc[o] + acc[mb][nb][i]);
             else
-              p.dh_acc[o] += acc[mb][nb][i];
+              atomicAdd(p.dh_acc + o, acc[mb][nb][i]);
           }
       }
     }
@@ -815,7 +816,6 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
     p.cot = cotangent;
     p.cot_scale = cotangent_scale;
     p.dh_acc = dh_acc;
-    p.dh = (bf16*)dhidden;
     p.dw = dweight;
     p.N = n;
     p.D = d;
@@ -846,6 +846,9 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
       flce_bwd_pipe_kernel<<<per_block * kBlocks, gemm::THREADS, 0, s>>>(p);
       GPTRIG_CHECK_LAUNCH();
     }
+    const int64_t total = (int64_t)n * d;
+    f32_to_bf16_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, (bf16*)dhidden, total);
+    GPTRIG_CHECK_LAUNCH();
     return GPTRIG_OK;
   }
   {
