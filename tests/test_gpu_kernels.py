@@ -93,7 +93,8 @@ def document_segments_of_lengths(sequence, seed):
 def test_attention_long_context_documents_match_oracle(S, scale):
     """The 8k context preset (``recipes/reference/config.yaml:18-21``: seq 8192,
     document masking, ``inverse_head_dim`` scale) and a non-128-aligned long
-    window, packed documents of 1..3000 tokens; tolerance 2e-2 x max(1, |ref|max)."""
+    window, packed documents of 1..3000 tokens; the north star's bf16 bound,
+    max-abs <= 2e-2 on o, dq, dk and dv (observed: o 1.6e-2, gradients <= 2e-3)."""
     from gptrig.kernels import flash_attention as fa
 
     B, H, D = 1, 2, 64
@@ -109,9 +110,9 @@ def test_attention_long_context_documents_match_oracle(S, scale):
     torch.cuda.synchronize()
     assert maxabs(lse, lse_ref) <= 2e-3
     for name, got, want in (("o", o, o_ref), ("dq", dq, dq_ref), ("dk", dk, dk_ref), ("dv", dv, dv_ref)):
-        bound = 2e-2 * max(1.0, float(want.float().abs().max()))
-        print(f"  {name}: max|diff| {maxabs(got, want):.3e} bound {bound:.3e}", flush=True)
-        assert maxabs(got, want) <= bound, name
+        print(f"  {name}: max|diff| {maxabs(got, want):.3e} (|ref| max {float(want.float().abs().max()):.3g})",
+              flush=True)
+        assert maxabs(got, want) <= 2e-2, name
 
 
 def test_attention_autograd_api_and_strided_inputs():
