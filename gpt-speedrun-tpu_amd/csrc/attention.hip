@@ -573,7 +573,9 @@ __global__ void __launch_bounds__(256, 4)
   xcd_map(blockIdx.x, nq, B * H, bh, qb);
   qb = nq - 1 - qb;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // Scalar, so the per-wave mask decisions below are uniform branches.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
   const int q0 = qb * kBlockM;
   const int qw0 = q0 + wave * 32;
@@ -623,17 +625,26 @@ __global__ void __launch_bounds__(256, 4)
     for (int kc = 0; kc < KC; ++kc) s = mfma32(at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl), qreg[kc], s);
     // Row max on raw scores (scale > 0); masked scores become -inf.
     const int kh0 = kv0 + 32 * sb;
-    const bool need_mask = (kh0 + 31 > qw0) || (kh0 + 32 > S) || kSeg;
     float mraw = -INFINITY;
+    if constexpr (kSeg) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (need_mask) {
+      for (int i = 0; i < 16; ++i) {
         const int key = kh0 + 8 * (i >> 2) + 4 * hl + (i & 3);
         bool vis = key <= my_q && key < S;
-        if (kSeg && vis) vis = seg[(size_t)b * S + key] == seg_q;
+        if (vis) vis = seg[(size_t)b * S + key] == seg_q;
         s[i] = vis ? s[i] : -INFINITY;
+        mraw = fmaxf(mraw, s[i]);
       }
-      mraw = fmaxf(mraw, s[i]);
+    } else {
+      // One uniform branch per half: element i holds key kh0 + 4hl + c_i,
+      // c_i = 8 (i / 4) + i % 4, visible while c_i <= min(my_q, S - 1) - kh0 - 4hl.
+      if ((kh0 + 31 > qw0) || (kh0 + 32 > S)) {
+        const int lim = min(my_q, S - 1) - kh0 - 4 * hl;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 8 * (i >> 2) + (i & 3) <= lim ? s[i] : -INFINITY;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mraw = fmaxf(mraw, s[i]);
     }
     mraw = fmaxf(mraw, __shfl_xor(mraw, 32));
     // Lazy rescaling: the running max (log2 units) only moves when a row's
