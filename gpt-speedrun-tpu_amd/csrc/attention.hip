@@ -619,7 +619,7 @@ __global__ void __launch_bounds__(256, 4)
   };
 
   // One 32-key half of a tile in buffer (kt, vt).
-  auto half = [&](const at64::lds_t* kt, const at64::lds_t* vt, int kv0, int sb) {
+  auto half = [&](const at64::lds_t* kt, const at64::lds_t* vt, int kv0, int sb) __attribute__((always_inline)) {
     f32x16 s = f32x16{};
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) s = mfma32(at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl), qreg[kc], s);
