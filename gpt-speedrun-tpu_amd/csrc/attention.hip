@@ -76,7 +76,8 @@ __global__ void __launch_bounds__(256, 2)
   xcd_map(blockIdx.x, nq, B * H, bh, qb);
   qb = nq - 1 - qb;  // heaviest (longest causal prefix) first
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform mask branches
   const int hl = lane >> 5, l32 = lane & 31;
   const int q0 = qb * kBlockM;
   const int qw0 = q0 + wave * 32;
@@ -148,19 +149,24 @@ __global__ void __launch_bounds__(256, 2)
           s[sb] = mfma32(a, qreg[kc], s[sb]);
         }
       }
-      const bool need_mask = (kv0 + kBlockN - 1 > qw0) || (kv0 + kBlockN > S) || seg;
+      // One uniform branch per tile (the diagonal, ragged and segmented tiles).
+      if ((kv0 + kBlockN - 1 > qw0) || (kv0 + kBlockN > S) || seg) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kv0 + 32 * sb + 8 * (i >> 2) + 4 * hl + (i & 3);
+            bool vis = key <= my_q && key < S;
+            if (seg && vis) vis = seg[(size_t)b * S + key] == seg_q;
+            s[sb][i] = vis ? s[sb][i] : -INFINITY;
+          }
+      }
       float mloc = kMinusBig;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float x = s[sb][i] * scale_log2;
-          if (need_mask) {
-            int key = kv0 + 32 * sb + 8 * (i >> 2) + 4 * hl + (i & 3);
-            bool vis = key <= my_q && key < S;
-            if (seg && vis) vis = seg[(size_t)b * S + key] == seg_q;
-            x = vis ? x : -INFINITY;
-          }
+          const float x = s[sb][i] * scale_log2;
           s[sb][i] = x;
           mloc = fmaxf(mloc, x);
         }
