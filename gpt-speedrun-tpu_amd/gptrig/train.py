@@ -266,6 +266,14 @@ class GPTTrainer:
         self._ws: dict[str, torch.Tensor] = {}
         self.router_load = None  # [layers, experts] f32 of the last step (routed models)
         self.timers = None  # optional {name: list[(start_event, end_event)]}
+        # A layer's weight gradients can run as soon as the last micro-batch's
+        # backward has written that layer's output-gradients: they go to a
+        # second stream (default priority, like every stream here) and overlap
+        # the backward of the layers below, whose attention and elementwise
+        # launches leave the matrix cores partly idle.  One event per layer
+        # marks the point; the step's optimizer update waits for the stream.
+        self.wgrad_stream = torch.cuda.Stream(device=self.device)
+        self._layer_ready = [torch.cuda.Event() for _ in range(config.layers)]
 
     # -- helpers -----------------------------------------------------------------
     def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
@@ -438,7 +446,8 @@ class GPTTrainer:
                 xn1, rstd1 = xn1_next, rstd1_next
         return tok, seg, x, xf, rstdf, saved
 
-    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float, micro: int) -> None:
+    def _forward_backward(self, tokens: torch.Tensor, targets: torch.Tensor, loss_weight: float, micro: int,
+                          mark_layers: bool = False) -> None:
         c = self.config
         A = self.arena
         Bm, S = tokens.shape
@@ -520,6 +529,8 @@ class GPTTrainer:
                           dqkv[:, d:].data_ptr(), dqkv[:, 2 * d:].data_ptr(), attn_ws.data_ptr(), attn_ws.numel(),
                           Bm, H, S, D, bwd_strides.data_ptr(), self.scale, rope_c.data_ptr(), rope_s.data_ptr(),
                           stream)
+            if mark_layers:  # this layer's four output-gradients are written
+                self._layer_ready[i].record()
             dxn1 = torch.mm(dqkv, A.w(p + "qkv_w").t())
             below = lin_dout[i - 1]["mlp_down"] if (unit and i > 0 and not c.experts) else None
             dx, _ = rmsnorm_backward(dxn1, x_in, A.w(p + "ln1_scale"), rstd1, A.grad(p + "ln1_scale"), True,
@@ -555,10 +566,20 @@ class GPTTrainer:
         n_micro = x.shape[0] // mb
         weight = 1.0 / (n_micro * mb * x.shape[1])
         for j in range(n_micro):
-            self._forward_backward(x[j * mb:(j + 1) * mb], y[j * mb:(j + 1) * mb], weight, j)
-        for i in range(c.layers):
-            for name in self.linears:
-                self._weight_grad(f"blocks/{i}/{name}", self.lin_in[i][name], self.lin_dout[i][name])
+            self._forward_backward(x[j * mb:(j + 1) * mb], y[j * mb:(j + 1) * mb], weight, j,
+                                   mark_layers=j == n_micro - 1)
+        # Weight gradients on the second stream, each layer after its event
+        # (the layers finish top-down).  They write only the block linears'
+        # gradient rows, which nothing on the main stream touches until the
+        # optimizer update.
+        main = torch.cuda.current_stream(self.device)
+        side = self.wgrad_stream
+        for i in reversed(range(c.layers)):
+            side.wait_event(self._layer_ready[i])
+            with torch.cuda.stream(side):
+                for name in self.linears:
+                    self._weight_grad(f"blocks/{i}/{name}", self.lin_in[i][name], self.lin_dout[i][name])
+        main.wait_stream(side)
         self.step_count += 1
         step = self.step_count
         lr = learning_rate(step, c.optimizer)
