@@ -59,6 +59,43 @@ __device__ __forceinline__ float2 column_stats(f32x16 (&acc)[4][2], int nb, int 
   return make_float2(mx, sum);
 }
 
+// Kept probabilities are fp16: values in (0, 1] with 3 more mantissa bits than
+// bf16 (what underflows is below 2^-24 of its column's max).
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+
+// column_stats that also stores every fp16 exp2(logit * log2(e) - max) of the
+// column (this wave's 128 vocabulary rows x one token) at col + 32 * row, for
+// the rows below vlim (the storage vocabulary): the kept-softmax forward.
+// Nothing is stored for a column with no real row.
+template <bool kMask>
+__device__ __forceinline__ float2 column_stats_keep(f32x16 (&acc)[4][2], int nb, int lim, int vlim, f16* col) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float y = (!kMask || 32 * mb + 8 * (i >> 2) + (i & 3) < lim) ? acc[mb][nb][i] * GPTRIG_LOG2E : -INFINITY;
+      acc[mb][nb][i] = y;
+      mx = fmaxf(mx, y);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float sum = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = fast_exp2(acc[mb][nb][i] - mx);
+        sum += p;
+        const int r = 32 * mb + 8 * (i >> 2) + (i & 3);
+        if (!kMask || r < vlim) col[32 * r] = (f16)p;
+      }
+  }
+  sum += __shfl_xor(sum, 32);
+  return make_float2(mx, sum);
+}
+
 // ---------------------------------------------------------------------------
 // Forward: partial (max, sum exp) in the log2 domain per token over the tile.
 // ---------------------------------------------------------------------------
@@ -97,8 +134,16 @@ __global__ void __launch_bounds__(gemm::THREADS)
 // one workgroup per CU walks the tiles, copying the next tile's first stages
 // while this one's epilogue runs.  Same epilogue as flce_fwd_kernel, with
 // LDS-only barriers (a full __syncthreads would wait for those copies).
+// kKeep (the kept-softmax forward): every probability exp2(y - m) of the
+// tile, m the max over its wave's 128 vocabulary rows, is also stored as fp16
+// in the blocked G^T layout of the one-chunk backward (element (v, n) at
+// ((n / 32) * V + v) * 32 + n % 32, v < V), and m at
+// mhalf[(2 tile + half) * N + n], so the backward rescales them instead of
+// recomputing the logits.
+template <bool kKeep>
 __global__ void __launch_bounds__(gemm::THREADS)
-    flce_fwd_persistent_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, float2* __restrict__ partial) {
+    flce_fwd_persistent_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, float2* __restrict__ partial,
+                               f16* __restrict__ keep, float* __restrict__ mhalf) {
   __shared__ float2 xchg[4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
@@ -113,7 +158,20 @@ __global__ void __launch_bounds__(gemm::THREADS)
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const int n = tn * BN + 64 * wn + 32 * nb + l32;
-      const float2 st = full ? column_stats<false>(acc, nb, lim) : column_stats<true>(acc, nb, lim);
+      float2 st;
+      if constexpr (kKeep) {
+        // Tokens past n are not stored: their column points at row 0.
+        f16* col = keep + (n < N ? ((size_t)(n >> 5) * V + vbase + 4 * hl) * 32 + (n & 31) : 0);
+        const int vlim = V - vbase - 4 * hl;
+        if (n < N)
+          st = full ? column_stats_keep<false>(acc, nb, lim, vlim, col)
+                    : column_stats_keep<true>(acc, nb, lim, vlim, col);
+        else
+          st = full ? column_stats<false>(acc, nb, lim) : column_stats<true>(acc, nb, lim);
+        if (hl == 0 && n < N) mhalf[(size_t)(2 * tm + wm) * N + n] = st.x;
+      } else {
+        st = full ? column_stats<false>(acc, nb, lim) : column_stats<true>(acc, nb, lim);
+      }
       const float mx = st.x, sum = st.y;
       if (wm == 1 && hl == 0) xchg[wn][32 * nb + l32] = make_float2(mx, sum);
       GPTRIG_WAIT_LGKM0();
@@ -692,9 +750,66 @@ void* scratch_ptr() {
 }
 
 // The forward's launches (validated inputs, workspace of at least
-// gptrig_flce_fwd_workspace_bytes), shared by both entry points.
+// gptrig_flce_fwd_workspace_bytes), shared by the entry points; keep (with d
+// a multiple of 128) also stores the kept softmax of gptrig_flce_fwd_keep.
 int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
-                    void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s);
+                    void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s,
+                    void* keep = nullptr);
+
+// Kept-softmax buffer: the G^T array of the one-chunk backward ([ceil(n/32)]
+// blocks of [vocab][32]; fp16 probabilities from the forward, rewritten in
+// place as the bf16 gradient), then the f32 per-(half tile, token) maxima
+// [2 ceil(vocab/256)][n].
+size_t keep_gt_bytes(int n, int vocab) { return align256((size_t)vocab * ceil_div(n, 32) * 32 * sizeof(bf16)); }
+
+// Backward from the kept softmax, step 1: the per-(half tile, token) maxima m
+// become the factors a = exp2(m - lse log2(e)) ct of their probabilities (in
+// place), ct the token's cotangent (0 for an invalid target).
+__global__ void flce_keep_alpha_kernel(float* __restrict__ mh, int halves, int N, int sem_v,
+                                       const int32_t* __restrict__ targets, const float* __restrict__ lse,
+                                       const float* __restrict__ cot, float cot_scale) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)halves * N) return;
+  const int n = (int)(i % N);
+  const int t = targets[n];
+  const float ct = (t >= 0 && t < sem_v) ? (cot ? cot[n] : cot_scale) : 0.f;
+  const float m = mh[i];
+  mh[i] = m == -INFINITY ? 0.f : fast_exp2(m - lse[n] * GPTRIG_LOG2E) * ct;
+}
+
+// Step 2: G^T[v][n] = bf16(p a - [v == t] ct), zero for v >= semantic vocab
+// (K1's values, from the kept fp16 p instead of recomputed logits), in place:
+// blockIdx.y = the 32-token block, one thread per 8 tokens of one row,
+// consecutive threads on consecutive 16 bytes.
+__global__ void __launch_bounds__(256)
+    flce_keep_rescale_kernel(bf16* __restrict__ gt, const float* __restrict__ alpha, int N, int V, int sem_v,
+                             const int32_t* __restrict__ targets, const float* __restrict__ cot, float cot_scale) {
+  const int rem = blockIdx.x * 256 + threadIdx.x;
+  if (rem >= V * 4) return;
+  const int blk = blockIdx.y;
+  const int v = rem >> 2, c = rem & 3;
+  const int n0 = 32 * blk + 8 * c;
+  if (n0 >= N) return;  // N % 8 == 0: a group is wholly in or out
+  bf16* g = gt + ((size_t)blk * V + v) * 32 + 8 * c;
+  bf16x8 o = bf16x8{};
+  if (v < sem_v) {
+    const f16x8 p = *reinterpret_cast<const f16x8*>(g);
+    const float* a = alpha + (size_t)(2 * (v >> 8) + ((v >> 7) & 1)) * N + n0;
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(a);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(a + 4);
+    const i32x4_t t0 = *reinterpret_cast<const i32x4_t*>(targets + n0);
+    const i32x4_t t1 = *reinterpret_cast<const i32x4_t*>(targets + n0 + 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float aj = j < 4 ? a0[j] : a1[j - 4];
+      const int tj = j < 4 ? t0[j] : t1[j - 4];
+      float g8 = (float)p[j] * aj;
+      if (tj == v) g8 -= cot ? cot[n0 + j] : cot_scale;  // tj == v < sem_v: a valid target
+      o[j] = (bf16)g8;
+    }
+  }
+  *reinterpret_cast<bf16x8*>(g) = o;
+}
 
 }  // namespace
 
@@ -731,20 +846,45 @@ int gptrig_flce_fwd_noalloc(const void* hidden, const void* weight, const int32_
   return flce_fwd_launch(hidden, weight, targets, losses, lse, ws, n, d, vocab, semantic_vocab, (hipStream_t)stream);
 }
 
+size_t gptrig_flce_keep_bytes(int n, int vocab) {
+  if (n <= 0 || vocab <= 0) return 0;
+  return keep_gt_bytes(n, vocab) + align256((size_t)2 * ceil_div(vocab, BM) * n * sizeof(float));
+}
+
+int gptrig_flce_fwd_keep(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
+                         void* keep, size_t keep_bytes, void* workspace, size_t workspace_bytes, int n, int d,
+                         int vocab, int semantic_vocab, void* stream) {
+  if (!hidden || !weight || !targets || !losses || !lse || !keep || !workspace) return GPTRIG_E_NULL;
+  if (n <= 0 || d <= 0 || vocab <= 0 || d % 64) return GPTRIG_E_SHAPE;
+  if (d % (4 * gemm::BK)) return GPTRIG_E_UNSUPPORTED;  // the persistent forward only
+  if (n % 8) return GPTRIG_E_UNSUPPORTED;                // 16-byte token groups of the backward
+  if (semantic_vocab <= 0 || semantic_vocab > vocab) return GPTRIG_E_SHAPE;
+  if (workspace_bytes < gptrig_flce_fwd_workspace_bytes(n, d, vocab)) return GPTRIG_E_WORKSPACE;
+  if (keep_bytes < gptrig_flce_keep_bytes(n, vocab)) return GPTRIG_E_WORKSPACE;
+  if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)workspace | (uintptr_t)keep) & 15) return GPTRIG_E_SHAPE;
+  return flce_fwd_launch(hidden, weight, targets, losses, lse, workspace, n, d, vocab, semantic_vocab,
+                         (hipStream_t)stream, keep);
+}
+
 }  // extern "C"
 
 namespace {
 
 int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
-                    void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s) {
+                    void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s, void* keep) {
   const int ntiles = ceil_div(vocab, BM);
   float2* partial = (float2*)workspace;
   float* tlogit = (float*)((char*)workspace + align256((size_t)ntiles * n * sizeof(float2)));
   Operand W{(const bf16*)weight, d}, Hd{(const bf16*)hidden, d};
-  if (d % (4 * gemm::BK) == 0) {
+  if (keep) {
     const unsigned tiles = tiles_of(vocab, n), cus = (unsigned)gemm::device_cus();
-    flce_fwd_persistent_kernel<<<tiles < cus ? tiles : cus, gemm::THREADS, 0, s>>>(W, Hd, vocab, n, d, semantic_vocab,
-                                                                                   partial);
+    float* mh = (float*)((char*)keep + keep_gt_bytes(n, vocab));
+    flce_fwd_persistent_kernel<true><<<tiles < cus ? tiles : cus, gemm::THREADS, 0, s>>>(
+        W, Hd, vocab, n, d, semantic_vocab, partial, (f16*)keep, mh);
+  } else if (d % (4 * gemm::BK) == 0) {
+    const unsigned tiles = tiles_of(vocab, n), cus = (unsigned)gemm::device_cus();
+    flce_fwd_persistent_kernel<false><<<tiles < cus ? tiles : cus, gemm::THREADS, 0, s>>>(
+        W, Hd, vocab, n, d, semantic_vocab, partial, nullptr, nullptr);
   } else {
     flce_fwd_kernel<<<tiles_of(vocab, n), gemm::THREADS, 0, s>>>(W, Hd, vocab, n, d, semantic_vocab, partial);
   }
@@ -882,6 +1022,70 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
                                                                                         dh_acc, d, 2, nullptr);
     GPTRIG_CHECK_LAUNCH();
   }
+  const int64_t total = (int64_t)n * d;
+  f32_to_bf16_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, (bf16*)dhidden, total);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+size_t gptrig_flce_bwd_keep_workspace_bytes(int n, int d) {
+  if (n <= 0 || d <= 0) return 0;
+  return align256((size_t)n * d * sizeof(float));
+}
+
+// The one-chunk backward from gptrig_flce_fwd_keep's kept softmax: the G^T
+// values come from rescaling the kept probabilities (two bandwidth passes)
+// instead of recomputing the logits GEMM; then the same dW and dh GEMMs.
+int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
+                         const float* cotangent, float cotangent_scale, void* dhidden, float* dweight,
+                         int accumulate_dweight, void* keep, size_t keep_bytes, void* workspace,
+                         size_t workspace_bytes, int n, int d, int vocab, int semantic_vocab, void* stream) {
+  if (!hidden || !weight || !targets || !lse || !dhidden || !dweight || !keep || !workspace) return GPTRIG_E_NULL;
+  if (n <= 0 || d <= 0 || vocab <= 0 || d % 64) return GPTRIG_E_SHAPE;
+  if (semantic_vocab <= 0 || semantic_vocab > vocab) return GPTRIG_E_SHAPE;
+  if (n % 8) return GPTRIG_E_UNSUPPORTED;
+  if (keep_bytes < gptrig_flce_keep_bytes(n, vocab)) return GPTRIG_E_WORKSPACE;
+  if (workspace_bytes < gptrig_flce_bwd_keep_workspace_bytes(n, d)) return GPTRIG_E_WORKSPACE;
+  if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)workspace | (uintptr_t)dweight | (uintptr_t)keep |
+       (uintptr_t)targets) & 15)
+    return GPTRIG_E_SHAPE;  // (the rescale reads targets 16 bytes at a time)
+  if (ceil_div(n, 32) > 65535) return GPTRIG_E_UNSUPPORTED;  // grid.y of the rescale
+  hipStream_t s = (hipStream_t)stream;
+  bf16* gt = (bf16*)keep;
+  float* alpha = (float*)((char*)keep + keep_gt_bytes(n, vocab));
+  float* dh_acc = (float*)workspace;
+  const bf16* Wp = (const bf16*)weight;
+  const bf16* Hp = (const bf16*)hidden;
+  if (!accumulate_dweight) {
+    const int64_t total = (int64_t)vocab * d;
+    zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
+    GPTRIG_CHECK_LAUNCH();
+  }
+  {
+    const int64_t total = (int64_t)n * d;
+    zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, total);
+    GPTRIG_CHECK_LAUNCH();
+  }
+  const int halves = 2 * ceil_div(vocab, BM);
+  flce_keep_alpha_kernel<<<ceil_div((int64_t)halves * n, 256), 256, 0, s>>>(alpha, halves, n, semantic_vocab, targets,
+                                                                            lse, cotangent, cotangent_scale);
+  GPTRIG_CHECK_LAUNCH();
+  const dim3 rgrid((unsigned)ceil_div(vocab * 4, 256), (unsigned)ceil_div(n, 32));
+  flce_keep_rescale_kernel<<<rgrid, 256, 0, s>>>(gt, alpha, n, vocab, semantic_vocab, targets, cotangent,
+                                                  cotangent_scale);
+  GPTRIG_CHECK_LAUNCH();
+  // dW += G^T h and dh += G W, as in gptrig_flce_bwd's one-chunk path.
+  const int vc = vocab;
+  Operand Ag{gt, n, vc}, Bh{Hp, d};
+  const int dw_split = gemm::choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
+  gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(Ag, Bh, vc, d, n, dw_split,
+                                                                                      dweight, d, 2, nullptr);
+  GPTRIG_CHECK_LAUNCH();
+  Operand Agt{gt, n, vc}, Bw{Wp, d};
+  const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
+  gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
+                                                                                      dh_acc, d, 2, nullptr);
+  GPTRIG_CHECK_LAUNCH();
   const int64_t total = (int64_t)n * d;
   f32_to_bf16_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, (bf16*)dhidden, total);
   GPTRIG_CHECK_LAUNCH();

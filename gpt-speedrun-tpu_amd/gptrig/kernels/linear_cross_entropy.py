@@ -114,6 +114,45 @@ def flce_backward(h2, w, t1, lse, cotangent, cotangent_scale: float, semantic_vo
     return dh, dweight
 
 
+def flce_forward_keep(h2: torch.Tensor, w: torch.Tensor, t1: torch.Tensor, semantic_vocab_size: int,
+                      keep: torch.Tensor | None = None):
+    """``flce_forward`` that also keeps the probabilities for
+    ``flce_backward_keep`` (``gptrig_flce_fwd_keep``): returns ``(losses, lse,
+    keep)``, ``keep`` a uint8 device buffer of ``gptrig_flce_keep_bytes``
+    (passed in to reuse one)."""
+
+    n, d = h2.shape
+    V = w.shape[0]
+    losses = torch.empty(n, dtype=torch.float32, device=h2.device)
+    lse = torch.empty(n, dtype=torch.float32, device=h2.device)
+    nbytes = _lib.query("gptrig_flce_keep_bytes", n, V)
+    if keep is None or keep.numel() < nbytes:
+        keep = _lib.workspace(nbytes, h2.device)
+    ws = _lib.workspace(_lib.query("gptrig_flce_fwd_workspace_bytes", n, d, V), h2.device)
+    _lib.call("gptrig_flce_fwd_keep", h2.data_ptr(), w.data_ptr(), t1.data_ptr(), losses.data_ptr(), lse.data_ptr(),
+              keep.data_ptr(), keep.numel(), ws.data_ptr(), ws.numel(), n, d, V, int(semantic_vocab_size),
+              _lib.stream())
+    return losses, lse, keep
+
+
+def flce_backward_keep(h2, w, t1, lse, keep, cotangent, cotangent_scale: float, semantic_vocab_size: int,
+                       dweight: torch.Tensor | None = None, accumulate: bool = False):
+    """``flce_backward`` from ``flce_forward_keep``'s buffer (consumed)."""
+
+    n, d = h2.shape
+    V = w.shape[0]
+    dh = torch.empty((n, d), dtype=torch.bfloat16, device=h2.device)
+    if dweight is None:
+        dweight = torch.empty((V, d), dtype=torch.float32, device=h2.device)
+        accumulate = False
+    ws = _lib.workspace(_lib.query("gptrig_flce_bwd_keep_workspace_bytes", n, d), h2.device)
+    _lib.call("gptrig_flce_bwd_keep", h2.data_ptr(), w.data_ptr(), t1.data_ptr(), lse.data_ptr(),
+              _lib.ptr(cotangent), float(cotangent_scale), dh.data_ptr(), dweight.data_ptr(), int(accumulate),
+              keep.data_ptr(), keep.numel(), ws.data_ptr(), ws.numel(), n, d, V, int(semantic_vocab_size),
+              _lib.stream())
+    return dh, dweight
+
+
 def _flatten(hidden, embedding, targets):
     """bf16 ``[n8, d64]`` hidden, bf16 ``[V, d64]`` weight and int32 targets:
     rows padded to a multiple of 8 with target -1 (an invalid target: no loss,

@@ -75,8 +75,9 @@ class GPTConfig:
     router_aux_coefficient: float = 0.01
     # The backward's FLCE vocabulary chunk: True = one chunk over the whole
     # vocabulary while its bf16 [tokens, vocab] gradient fits 8 GiB (the
-    # fastest choice on one MI355X); False = vocab_tile_size, the reference's
-    # bounded [tokens, tile] working set.
+    # fastest choice on one MI355X), with the forward keeping its
+    # probabilities in that array so the backward skips the logits recompute;
+    # False = vocab_tile_size, the reference's bounded [tokens, tile] working set.
     flce_whole_vocab: bool = True
     optimizer: OptimizerConfig = field(default_factory=OptimizerConfig)
 
@@ -465,10 +466,22 @@ class GPTTrainer:
         losses = torch.empty(N, dtype=F32, device=self.device)
         lse_ce = torch.empty(N, dtype=F32, device=self.device)
         ws = self._workspace("flce_fwd", _lib.query("gptrig_flce_fwd_workspace_bytes", N, d, c.vocab_size))
+        # With the whole-vocabulary opt-in the forward keeps its probabilities
+        # (fp16 [vocab, N]) and the backward rescales them instead of
+        # recomputing the logits GEMM.
+        keep = None
+        if (c.flce_whole_vocab and d % 128 == 0 and N % 8 == 0
+                and lce.grad_chunk(N, c.vocab_size) >= c.vocab_size):
+            keep = self._workspace("flce_keep", _lib.query("gptrig_flce_keep_bytes", N, c.vocab_size))
         with self._timed("flce"):
-            _lib.call("gptrig_flce_fwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
-                      lse_ce.data_ptr(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size,
-                      stream)
+            if keep is not None:
+                _lib.call("gptrig_flce_fwd_keep", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
+                          lse_ce.data_ptr(), keep.data_ptr(), keep.numel(), ws.data_ptr(), ws.numel(), N, d,
+                          c.vocab_size, c.semantic_vocab_size, stream)
+            else:
+                _lib.call("gptrig_flce_fwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
+                          lse_ce.data_ptr(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size,
+                          stream)
         _lib.call("gptrig_weighted_sum", losses.data_ptr(), N, loss_weight, self.loss.data_ptr(), stream)
         if c.experts:
             # The per-layer expert load of the step (the reference's router row,
@@ -482,13 +495,21 @@ class GPTTrainer:
         # ---- backward ----
         # One vocabulary chunk while the bf16 G^T fits the budget (6.6 GB at
         # 65536 tokens x 50304), unless the config asks for the bounded tile.
-        chunk = lce.grad_chunk(N, c.vocab_size) if c.flce_whole_vocab else lce.chunk_for(c.vocab_tile_size)
-        ws = self._workspace("flce_bwd", _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
         dxf = torch.empty((N, d), dtype=BF16, device=self.device)
-        with self._timed("flce"):
-            _lib.call("gptrig_flce_bwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(), None,
-                      loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, ws.data_ptr(), ws.numel(),
-                      N, d, c.vocab_size, c.semantic_vocab_size, chunk, stream)
+        if keep is not None:
+            ws = self._workspace("flce_bwd_keep", _lib.query("gptrig_flce_bwd_keep_workspace_bytes", N, d))
+            with self._timed("flce"):
+                _lib.call("gptrig_flce_bwd_keep", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(),
+                          None, loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, keep.data_ptr(),
+                          keep.numel(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size, stream)
+        else:
+            chunk = lce.grad_chunk(N, c.vocab_size) if c.flce_whole_vocab else lce.chunk_for(c.vocab_tile_size)
+            ws = self._workspace("flce_bwd",
+                                 _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
+            with self._timed("flce"):
+                _lib.call("gptrig_flce_bwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(), None,
+                          loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, ws.data_ptr(),
+                          ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size, chunk, stream)
         unit = self.residual_scale == 1.0
         top = lin_dout[c.layers - 1]["mlp_down"] if unit and not c.experts else None
         dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True, out=top)

@@ -115,14 +115,39 @@ int gptrig_flce_fwd_noalloc(const void* hidden, const void* weight, const int32_
  * vocab_tile_size) is the vocabulary chunk whose logits are recomputed at a
  * time: the workspace holds one bf16 [n, vocab_chunk] logit gradient, the f32
  * [n, d] dh accumulator of the reference's loop (:247) and, with more than one
- * chunk, a few KB of work-queue counters.  Several chunks run as one
- * persistent launch; a chunk covering the whole vocabulary (vocab_chunk >=
+ * chunk, a few KB of work-queue counters.  Several chunks run as pipelined
+ * launches (each recomputes one half of the buffer while the dW / dh products
+ * read the other); a chunk covering the whole vocabulary (vocab_chunk >=
  * vocab) runs as three launches with no accumulator passes. */
 size_t gptrig_flce_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk);
 int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
                     const float* cotangent, float cotangent_scale, void* dhidden, float* dweight,
                     int accumulate_dweight, void* workspace, size_t workspace_bytes, int n, int d, int vocab,
                     int semantic_vocab, int vocab_chunk, void* stream);
+
+/* Kept-softmax forward and backward: the one-chunk backward without the
+ * logits recompute.  The reference's backward recomputes the logits tile by
+ * tile from the saved (hidden, weight) (rig/kernels/linear_cross_entropy.py:
+ * 220-302); this pair instead keeps the forward's probabilities for the
+ * backward, as fp16 exp(logit - m) with m the max over 128 vocabulary rows,
+ * plus m: a [vocab, n] 16-bit array, so a caller that can hold it (the
+ * trainer's whole-vocabulary opt-in, 6.6 GB at 65536 tokens) trades the
+ * recompute GEMM for two bandwidth passes.  Same losses and lse as
+ * gptrig_flce_fwd; gradient values as gptrig_flce_bwd's up to one fp16
+ * rounding of each probability before its bf16 rounding.  d a multiple of 128 and n of 8 (else
+ * GPTRIG_E_UNSUPPORTED).  keep: gptrig_flce_keep_bytes(n, vocab) bytes, 16-byte
+ * aligned, written by the forward and consumed (overwritten) by the backward,
+ * which must see the forward's lse.  The backward's workspace is the f32
+ * [n, d] dh accumulator. */
+size_t gptrig_flce_keep_bytes(int n, int vocab);
+int gptrig_flce_fwd_keep(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
+                         void* keep, size_t keep_bytes, void* workspace, size_t workspace_bytes, int n, int d,
+                         int vocab, int semantic_vocab, void* stream);
+size_t gptrig_flce_bwd_keep_workspace_bytes(int n, int d);
+int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* targets, const float* lse,
+                         const float* cotangent, float cotangent_scale, void* dhidden, float* dweight,
+                         int accumulate_dweight, void* keep, size_t keep_bytes, void* workspace,
+                         size_t workspace_bytes, int n, int d, int vocab, int semantic_vocab, void* stream);
 
 /* ------------------------------------------------------------------------
  * RMSNorm, rig/nn.py:26-33 (rms_norm): y = bf16(bf16(x*rsqrt(mean(x^2)+1e-5)) * scale).

@@ -48,6 +48,15 @@ def test_host_validation_rejects_bad_arguments_without_launching():
     assert lib.gptrig_flce_fwd(dummy, dummy, dummy, dummy, dummy, dummy, 1 << 30, 8, 128, 10, 11, None) == -2
     # FLCE: workspace too small
     assert lib.gptrig_flce_fwd(dummy, dummy, dummy, dummy, dummy, dummy, 16, 8, 128, 10, 10, None) == -6
+    # FLCE kept softmax: width a multiple of 64 but not 128, keep buffer too small, tokens not a multiple of 8
+    big = ctypes.c_size_t(1 << 40)
+    assert lib.gptrig_flce_fwd_keep(dummy, dummy, dummy, dummy, dummy, dummy, big, dummy, big, 16, 64, 1000, 1000,
+                                    None) == -4
+    assert lib.gptrig_flce_fwd_keep(dummy, dummy, dummy, dummy, dummy, dummy, 16, dummy, big, 16, 128, 1000, 1000,
+                                    None) == -6
+    assert lib.gptrig_flce_bwd_keep(dummy, dummy, dummy, dummy, None, ctypes.c_float(1.0), dummy, dummy, 0, dummy,
+                                    big, dummy, big, 12, 128, 1000, 1000, None) == -4
+    assert lib.gptrig_flce_keep_bytes(16, 1000) >= 2 * 32 * 1000 + 2 * 4 * 16 * 4
     # AdamW: chunk not a multiple of 1024
     assert lib.gptrig_adamw(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 1000, 0.1, 0.9, 0.95, 1, None, None,
                             None) == -2

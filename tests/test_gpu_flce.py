@@ -1,12 +1,13 @@
-"""GPU parity of the FLCE backward's two paths, through the C ABI (ctypes).
+"""GPU parity of the FLCE backward's paths, through the C ABI (ctypes).
 
 * the chunked backward (several vocabulary chunks: the public API's default
   ``vocab_tile_size`` = 2048, pipelined launches over two halves of the
-  ``[tokens, chunk]`` buffer) and the one-chunk launches (the trainer's
-  whole-vocabulary opt-in) against the CPU oracle
-  (``oracle.flce``, restating ``rig/kernels/linear_cross_entropy.py``), at
-  config C's full size (16384 tokens x 768 x 50304) and at small ragged
-  shapes;
+  ``[tokens, chunk]`` buffer), the one-chunk launches and the kept-softmax
+  pair (the trainer's whole-vocabulary opt-in: the forward keeps its fp16
+  probabilities, the backward rescales them instead of recomputing the
+  logits) against the CPU oracle (``oracle.flce``, restating
+  ``rig/kernels/linear_cross_entropy.py``), at config C's full size (16384
+  tokens x 768 x 50304) and at small ragged shapes;
 * the reference's width-5 bfloat16 fixture (``tests/test_linear_cross_entropy.py:
   73-80,129-152``), through the zero-padded public API.
 
@@ -97,6 +98,67 @@ def test_config_c_pipelined_default_tile_matches_oracle():
     assert maxabs(dw1, dw_ref) <= 2e-2 * sw
     # The two paths sum the same bf16 products in different fp32 orders.
     assert maxabs(dh1, hg.grad) <= 1e-2 * sh
+    # Kept-softmax pair (the trainer's path): same losses as the forward, and
+    # gradients from the rescaled kept probabilities.
+    print("GPU kept softmax", flush=True)
+    lk, lsek, dhk, dwk = run_keep(h, w, t, V, scale=1.0 / n)
+    assert abs(float(lk.mean()) - want) <= 1e-3 * abs(want)
+    assert maxabs(dhk, dh_ref) <= 2e-2 * sh
+    assert maxabs(dwk, dw_ref) <= 2e-2 * sw
+    assert maxabs(dhk, dh1) <= 1e-2 * sh and maxabs(dwk, dw1) <= 1e-2 * sw
+
+
+def run_keep(h, w, t, sv, ct=None, scale=0.0, dweight=None, accumulate=False):
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    hg, wg, tg = h.to(DEV), w.to(torch.bfloat16).to(DEV), t.to(DEV)
+    losses, lse, keep = lce.flce_forward_keep(hg, wg, tg, sv)
+    dh, dw = lce.flce_backward_keep(hg, wg, tg, lse, keep, None if ct is None else ct.to(DEV), scale, sv,
+                                    dweight=dweight, accumulate=accumulate)
+    torch.cuda.synchronize()
+    return losses.cpu(), lse.cpu(), dh.cpu(), dw.cpu()
+
+
+KEEP_CASES = [
+    # (n, d, V, semantic V): ragged vocabulary tiles and a partial last token tile; d a multiple of 128
+    (2056, 256, 1300, 1297),
+    (4096, 768, 5000, 4999),
+    (8, 128, 600, 600),
+    (1536, 384, 2311, 2000),
+]
+
+
+@pytest.mark.parametrize("n,d,V,sv", KEEP_CASES)
+def test_kept_softmax_pair_matches_oracle_and_forward(n, d, V, sv):
+    """gptrig_flce_fwd_keep / gptrig_flce_bwd_keep: the forward's losses and
+    lse equal gptrig_flce_fwd's bit for bit (same launches plus stores), and
+    the gradients from the rescaled kept probabilities match the oracle to the
+    tolerances of the recompute path (one more fp16 rounding per probability),
+    with invalid targets, per-token cotangents, padding rows and dW
+    accumulation."""
+    print(f"flce kept case n={n} d={d} V={V} sv={sv}", flush=True)
+    h, w, t = inputs(n, d, V, sv, 71, 0.5, 0.5)
+    t[::11] = -1
+    g = torch.Generator().manual_seed(72)
+    ct = torch.rand(n, generator=g)
+    losses_ref, lse_ref = oflce.losses_and_lse(h, w, t, semantic_vocab_size=sv, vocab_tile_size=256)
+    dh_ref, dw_ref = oflce.losses_backward(h, w, t, lse_ref, ct, semantic_vocab_size=sv, vocab_tile_size=256)
+    lo, ls, _, _ = run_backward(h, w, t, sv, 1 << 20, ct=ct)
+    lk, lsk, dhk, dwk = run_keep(h, w, t, sv, ct=ct)
+    assert torch.equal(torch.isfinite(lk), torch.isfinite(lo))
+    fin = torch.isfinite(lo)
+    assert torch.equal(lk[fin], lo[fin]) and torch.equal(lsk, ls)
+    sh, sw = float(dh_ref.float().abs().max()), float(dw_ref.abs().max())
+    print(f"  dh {maxabs(dhk, dh_ref) / sh:.4f}, dW {maxabs(dwk, dw_ref) / sw:.4f} of max", flush=True)
+    assert maxabs(dhk, dh_ref) <= 2e-2 * sh
+    assert maxabs(dwk, dw_ref) <= 2e-2 * sw
+    assert (dwk[sv:] == 0).all()
+    base = torch.randn(V, d, generator=g)
+    _, _, dh2, dw2 = run_keep(h, w, t, sv, ct=ct, dweight=base.to(DEV), accumulate=True)
+    # (The one-chunk dh GEMM adds its K splits with f32 atomics: equal up to
+    # the order of those adds, one bf16 step at most.)
+    assert maxabs(dh2, dhk) <= 1e-2 * sh
+    assert maxabs(dw2 - base, dwk) <= 1e-5 * max(1.0, float(base.abs().max()))
 
 
 CHUNKED_CASES = [
