@@ -34,13 +34,13 @@ import torch  # noqa: E402
 
 METRIC = "train tokens/s at 125M S=1024; attn-bwd + FLCE TFLOP/s as % of bf16 MFMA peak"
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-# HBM bytes of one FLCE fwd+bwd launch sequence, by micro-batch tokens N (d 768,
-# V 50304, one vocabulary chunk): FETCH_SIZE (x 2.0, the factor the counter
+# HBM bytes of one FLCE fwd+bwd launch sequence (the trainer's kept-softmax
+# pair), by micro-batch tokens N (d 768, V 50304): FETCH_SIZE (x 2.0, the factor the counter
 # reads for a 256 MiB copy) + WRITE_SIZE (x 1.0) summed over its launches, from
 # `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes; a shape without a measurement reports null.
-FLCE_TRAFFIC_BYTES = {65536: (31412 + 7459) * 2 ** 20}
+FLCE_TRAFFIC_BYTES = {65536: (31112 + 13942) * 2 ** 20}
 
 
 def parse_args():
@@ -76,8 +76,10 @@ def traffic_pass(micro_batch: int) -> None:
     h = torch.randn(n, d, device=dev).bfloat16()
     w = (torch.randn(vocab, d, device=dev) * 0.02).bfloat16()
     t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32)
-    _, lse = lce.flce_forward(h, w, t, vocab)
-    lce.flce_backward(h, w, t, lse, None, 1.0 / n, vocab, lce.grad_chunk(n, vocab))
+    # The trainer's FLCE sequence: the kept-softmax forward and backward.
+    _, lse, keep = lce.flce_forward_keep(h, w, t, vocab)
+    lce.flce_backward_keep(h, w, t, lse, keep, None, 1.0 / n, vocab)
+    del keep
     torch.cuda.synchronize()
     q, k, v, do = (torch.randn(micro_batch, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
     o, lse2 = fa.flash_forward(q, k, v, None, 0.125)
@@ -150,10 +152,22 @@ def isolated_configs(reps: int = 20) -> dict:
             lce.flce_backward(h, w, t, lse_c, None, 1.0 / n, vocab, chunk)
         return run
 
-    # The trainer's whole-vocabulary chunk, and the public API's default
-    # vocab_tile_size (2048: the reference's bounded [tokens, tile] working set).
-    flce_ms = timed(flce_with(lce.grad_chunk(n, vocab)))
+    keep_buf = []
+
+    def flce_keep():
+        _, lse_c, kb = lce.flce_forward_keep(h, w, t, vocab, keep_buf[0] if keep_buf else None)
+        if not keep_buf:
+            keep_buf.append(kb)
+        lce.flce_backward_keep(h, w, t, lse_c, kb, None, 1.0 / n, vocab)
+
+    # The trainer's path (whole vocabulary, kept softmax), the same chunk with
+    # the logits recomputed, and the public API's default vocab_tile_size
+    # (2048: the reference's bounded [tokens, tile] working set).
+    flce_ms = timed(flce_keep)
     flce_tf = flce_flops(n, d, vocab) / (flce_ms / 1e3) / 1e12
+    keep_buf.clear()
+    whole_ms = timed(flce_with(lce.grad_chunk(n, vocab)))
+    whole_tf = flce_flops(n, d, vocab) / (whole_ms / 1e3) / 1e12
     tile_ms = timed(flce_with(lce.chunk_for(lce.DEFAULT_VOCAB_TILE_SIZE)))
     tile_tf = flce_flops(n, d, vocab) / (tile_ms / 1e3) / 1e12
     peak = MFMA_BF16_PEAK_TFLOPS
@@ -164,7 +178,10 @@ def isolated_configs(reps: int = 20) -> dict:
             "bwd_algorithmic_flops": attn_bwd_flops(B, H, S, D)},
         "flce_N16384_d768_V50304": {"ms": round(flce_ms, 4), "tflops": round(flce_tf, 1),
                                     "frac": round(flce_tf / peak, 4), "algorithmic_flops": flce_flops(n, d, vocab),
-                                    "chunk": "whole vocabulary (the trainer's opt-in)",
+                                    "path": "whole vocabulary, kept softmax (the trainer's opt-in)",
+                                    "whole_vocabulary_recompute": {"ms": round(whole_ms, 4),
+                                                                   "tflops": round(whole_tf, 1),
+                                                                   "frac": round(whole_tf / peak, 4)},
                                     "default_tile_2048": {"ms": round(tile_ms, 4), "tflops": round(tile_tf, 1),
                                                           "frac": round(tile_tf / peak, 4),
                                                           "workspace_bytes": lce.workspace_bytes(n, d, vocab)}},
@@ -410,8 +427,8 @@ def main():
                                f"{cfg.micro_batch_size}, AdamW",
                    "global_batch": cfg.batch_size, "micro_batch": cfg.micro_batch_size, "seq_len": cfg.seq_len,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": f"flce (fused LM-head cross-entropy fwd+bwd, per {cfg.micro_batch_size}x1024-token "
-                               "micro-batch)",
+        "roofline": {"kernel": f"flce (fused LM-head cross-entropy fwd+bwd, kept softmax, per "
+                               f"{cfg.micro_batch_size}x1024-token micro-batch)",
                      "bound": "mfma", "achieved": round(flce_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flce_tf / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": traffic, "traffic_GBps": None if traffic is None else round(traffic / flce_ms / 1e6, 1),

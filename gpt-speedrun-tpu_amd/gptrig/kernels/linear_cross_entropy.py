@@ -145,6 +145,8 @@ def flce_backward_keep(h2, w, t1, lse, keep, cotangent, cotangent_scale: float, 
     if dweight is None:
         dweight = torch.empty((V, d), dtype=torch.float32, device=h2.device)
         accumulate = False
+    if t1.data_ptr() % 16:  # the backward reads the targets 16 bytes at a time
+        t1 = t1.clone()
     ws = _lib.workspace(_lib.query("gptrig_flce_bwd_keep_workspace_bytes", n, d), h2.device)
     _lib.call("gptrig_flce_bwd_keep", h2.data_ptr(), w.data_ptr(), t1.data_ptr(), lse.data_ptr(),
               _lib.ptr(cotangent), float(cotangent_scale), dh.data_ptr(), dweight.data_ptr(), int(accumulate),

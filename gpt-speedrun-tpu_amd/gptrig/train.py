@@ -457,6 +457,8 @@ class GPTTrainer:
         lin_dout = [{k: t[rows] for k, t in layer.items()} for layer in self.lin_dout]
         stream = _lib.stream()
         tgt = targets.reshape(-1).to(torch.int32).contiguous()
+        if tgt.data_ptr() % 16:  # a row slice of a window: the FLCE backward reads 16-byte groups
+            tgt = tgt.clone()
         tok, seg, x, xf, rstdf, saved = self._forward(tokens, micro)
         st_qkv = (S * 3 * d, D, 3 * d)
         st_o = (S * d, D, d)
