@@ -53,24 +53,31 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// GELU, tanh approximation (jax.nn.gelu(approximate=True)), in fp32.
-__device__ __forceinline__ float tanh_fast(float u) {
-  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-inf.  The
-  // reciprocal is v_rcp_f32 (1 ulp), not the IEEE division sequence: its error
-  // is far below the bf16 rounding of every caller's result.
-  float e = fast_exp2(2.0f * GPTRIG_LOG2E * u);
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-}
+// GELU, tanh approximation (jax.nn.gelu(approximate=True)), in fp32, written
+// with the logistic function: with u = k (x + c x^3), k = sqrt(2/pi),
+// c = 0.044715,
+//   0.5 x (1 + tanh u) = x s,      s = 1 / (1 + exp(-2u)),
+//   d/dx                = s (1 + x 2u' (1 - s)),   2u' = 2k (1 + 3c x^2).
+// exp(-2u) is one v_exp_f32 of x (a + b x^2) with the constants folded, and
+// 1 / (1 + e) one v_rcp_f32 (1 ulp, far below the bf16 rounding of every
+// caller's result): 5 and 10 full-rate operations plus the two
+// transcendentals, against 10 and 18 for the tanh form.  Both saturate like
+// the tanh form: e = inf gives s = 0 (gelu -> -0), e = 0 gives s = 1.
 __device__ __forceinline__ float gelu_f(float x) {
-  const float k = 0.7978845608028654f;  // sqrt(2/pi)
-  float u = k * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanh_fast(u));
+  constexpr float a = -2.0f * 0.7978845608028654f * GPTRIG_LOG2E;  // -2k log2(e)
+  constexpr float b = a * 0.044715f;
+  const float e = fast_exp2(x * __builtin_fmaf(x * x, b, a));
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 __device__ __forceinline__ float gelu_grad_f(float x) {
-  const float k = 0.7978845608028654f;
-  float u = k * (x + 0.044715f * x * x * x);
-  float t = tanh_fast(u);
-  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * 0.044715f * x * x);
+  constexpr float a = -2.0f * 0.7978845608028654f * GPTRIG_LOG2E;
+  constexpr float b = a * 0.044715f;
+  constexpr float a2 = 2.0f * 0.7978845608028654f;  // 2k
+  constexpr float b2 = a2 * 3.0f * 0.044715f;       // 6kc
+  const float x2 = x * x;
+  const float s = __builtin_amdgcn_rcpf(1.0f + fast_exp2(x * __builtin_fmaf(x2, b, a)));
+  const float w = x * __builtin_fmaf(x2, b2, a2);
+  return s * __builtin_fmaf(w, 1.0f - s, 1.0f);
 }
 
 // Workgroup barrier without the vmcnt(0)/lgkmcnt(0) drain of __syncthreads():

@@ -22,7 +22,9 @@
 // bf16(acc) + b and the rotation round exactly as the standalone passes
 // (gelu_fwd / gelu_bwd / rope kernels) do on a bf16 GEMM output.
 //
-// One workgroup per 256 x 256 tile, on the ping-pong main loop.
+// K a multiple of 128: the persistent main loop (one workgroup per CU walking
+// the tiles, the next tile's operands in flight during each epilogue).  Other
+// K: one workgroup per 256 x 256 tile, on the ping-pong main loop.
 #include "gemm_core.h"
 
 namespace {
@@ -153,6 +155,118 @@ __global__ void __launch_bounds__(gemm::THREADS)
   linear_epilogue<kEpi>(acc, tm, tn, F, N, e, bias_s);
 }
 
+// ---- persistent form ----
+//
+// One workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...;
+// the next tile's first four stages are copied while the current tile's
+// epilogue runs (gemm::persistent), so no tile pays the operand latency of a
+// fresh launch.  The stage ring is then busy during the epilogue, so the tile
+// leaves through a 32 KB band of its own, one 64-feature band at a time: band
+// p holds features 32p .. 32p + 31 of both M halves (accumulator block mb =
+// p of every wave) for all 256 tokens.  Band row r (a token) is 128 bytes =
+// 8 chunks of 8 features; chunk c (features 128 (c / 4) + 32p + 8 (c % 4))
+// sits at position c ^ (r % 8).
+constexpr int kBandFeat = 64;
+
+__device__ __forceinline__ int band_feature(int tm, int p, int c) {
+  return tm * BM + 128 * (c >> 2) + 32 * p + 8 * (c & 3);
+}
+
+template <int kEpi, bool kWK>
+__global__ void __launch_bounds__(gemm::THREADS)
+    linear_persistent_kernel(Operand W, Operand X, int F, int N, int K, int group, EpiArgs e) {
+  __shared__ __attribute__((aligned(1024))) bf16 band_s[BN * kBandFeat];
+  typedef __attribute__((address_space(3))) bf16 lds_bf16;
+  lds_bf16* const band = (lds_bf16*)band_s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31, wm = wave & 1, wn = wave >> 1;
+  const int ntiles = ((F + BM - 1) / BM) * ((N + BN - 1) / BN);
+  // Read-phase position of this thread: chunk c of rows r0 + 64 it.
+  const int c = tid & 7, r0 = tid >> 3;
+  auto coords = [&](int t, int& tm, int& tn) { gemm::tile_coords(t, F, N, tm, tn, group); };
+  auto pre = [](int, int) {};
+  auto epi = [&](f32x16(&acc)[4][2], int tm, int tn) {
+    // Per-pass inputs loaded one pass ahead: the saved pre-activation (kDGelu).
+    bf16x8 aux[2][4];
+    auto load_aux = [&](int p, bf16x8(&dst)[4]) {
+      if constexpr (kEpi == kDGelu) {
+        const int f = band_feature(tm, p, c);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const int tok = tn * BN + r0 + 64 * it;
+          dst[it] = (tok < N && f < F) ? *reinterpret_cast<const bf16x8*>(e.aux + (int64_t)tok * e.ldaux + f)
+                                       : bf16x8{};
+        }
+      }
+    };
+    load_aux(0, aux[0]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if (p < 3) load_aux(p + 1, aux[(p + 1) & 1]);
+      const int f = band_feature(tm, p, c);
+      bf16x8 b8{};
+      if constexpr (has_bias(kEpi))
+        if (e.bias && f < F)  // (the bias may sit at any 2-byte offset)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) b8[j] = e.bias[f + j];
+      // Write phase: bf16(acc) of block mb = p into the band.
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int r = 64 * wn + 32 * nb + l32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bf16x4 o;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = (bf16)acc[p][nb][4 * q + j];
+          *(__attribute__((address_space(3))) bf16x4*)(band + r * kBandFeat + 8 * ((4 * wm + q) ^ (r & 7)) + 4 * hl) =
+              o;
+        }
+      }
+      GPTRIG_WAIT_LGKM0();
+      wg_barrier();
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int r = r0 + 64 * it;
+        const int tok = tn * BN + r;
+        bf16x8 v = *(const __attribute__((address_space(3))) bf16x8*)(band + r * kBandFeat + 8 * (c ^ (r & 7)));
+        if (tok >= N || f >= F) continue;  // F % 8 == 0: f < F covers f .. f+7
+        if constexpr (has_bias(kEpi)) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] + (float)b8[j]);
+        }
+        if constexpr (kEpi == kGelu) {
+          bf16x8 g;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) g[j] = (bf16)gelu_f((float)v[j]);
+          *reinterpret_cast<bf16x8*>(e.act + (int64_t)tok * e.ldy + f) = g;
+        } else if constexpr (kEpi == kDGelu) {
+          const bf16x8 h = aux[p & 1][it];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] * gelu_grad_f((float)h[j]));
+        } else if constexpr (kEpi == kRope) {
+          if (f < e.rope_cols) {
+            const int half = e.head_dim >> 1;
+            const int i0 = (f % e.head_dim) >> 1;
+            const int64_t t0 = (int64_t)(tok % e.seq) * half + i0;
+            const bf16x4 c4 = *reinterpret_cast<const bf16x4*>(e.rcs + t0);
+            const bf16x4 s4 = *reinterpret_cast<const bf16x4*>(e.rsn + t0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bf16x2 rr = rope_pair((float)v[2 * j], (float)v[2 * j + 1], (float)c4[j], (float)s4[j]);
+              v[2 * j] = rr[0];
+              v[2 * j + 1] = rr[1];
+            }
+          }
+        }
+        *reinterpret_cast<bf16x8*>(e.y + (int64_t)tok * e.ldy + f) = v;
+      }
+      GPTRIG_WAIT_LGKM0();
+      wg_barrier();  // every wave has read the band before the next pass writes it
+    }
+  };
+  gemm::persistent<kWK, true>(W, X, F, N, K, ntiles, coords, pre, epi);
+}
+
 template <int kEpi>
 int launch_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_kmajor, int n, int k, int f,
                   const EpiArgs& e, hipStream_t s) {
@@ -165,6 +279,16 @@ int launch_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int w_
   const Operand W{(const bf16*)w, ldw}, X{(const bf16*)x, ldx};
   const unsigned tiles = (unsigned)(ceil_div(f, BM) * ceil_div(n, BN));
   const int group = gemm::kGroupM;
+  if (k % (4 * gemm::BK) == 0) {
+    const unsigned grid = tiles < (unsigned)gemm::device_cus() ? tiles : (unsigned)gemm::device_cus();
+    const int pgroup = ceil_div(f, BM) <= 16 ? ceil_div(f, BM) : group;
+    if (w_kmajor)
+      linear_persistent_kernel<kEpi, true><<<grid, gemm::THREADS, 0, s>>>(W, X, f, n, k, pgroup, e);
+    else
+      linear_persistent_kernel<kEpi, false><<<grid, gemm::THREADS, 0, s>>>(W, X, f, n, k, pgroup, e);
+    GPTRIG_CHECK_LAUNCH();
+    return GPTRIG_OK;
+  }
   if (w_kmajor)
     linear_tile_kernel<kEpi, true><<<tiles, gemm::THREADS, 0, s>>>(W, X, f, n, k, group, e);
   else
