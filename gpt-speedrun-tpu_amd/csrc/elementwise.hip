@@ -32,7 +32,7 @@ template <bool kAdd>
 __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* x, const bf16* __restrict__ scale,
                                                           bf16* __restrict__ y, float* __restrict__ rstd, int rows,
                                                           int d, const bf16* __restrict__ branch, float branch_scale,
-                                                          bf16* sum_out) {
+                                                          bf16* sum_out, const bf16* __restrict__ branch_bias) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;
@@ -47,7 +47,12 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* x, const b
     if (c < chunks) {
       xv[t] = *reinterpret_cast<const bf16x4*>(xr + 4 * c);
       if (kAdd) {
-        const bf16x4 bv = *reinterpret_cast<const bf16x4*>(branch + (size_t)row * d + 4 * c);
+        bf16x4 bv = *reinterpret_cast<const bf16x4*>(branch + (size_t)row * d + 4 * c);
+        if (branch_bias) {  // the linear's own bias add, rounded before the residual add
+          const bf16x4 bb = *reinterpret_cast<const bf16x4*>(branch_bias + 4 * c);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bv[j] = (bf16)((float)bv[j] + (float)bb[j]);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) xv[t][j] = (bf16)((float)xv[t][j] + (float)(bf16)((float)bv[j] * branch_scale));
         *reinterpret_cast<bf16x4*>(sum_out + (size_t)row * d + 4 * c) = xv[t];
@@ -291,6 +296,44 @@ __global__ void __launch_bounds__(256) bias_grad_kernel(const bf16* __restrict__
 // ----------------------------------------------------------------------------
 // GELU, tanh approximation (jax.nn.gelu(approximate=True), train.py:1171)
 // ----------------------------------------------------------------------------
+// With a bias (the up-projection's, rig/nn.py:55-56): the GEMM output x gets
+// bf16(x + b[column]) first, the rounding of the linear's bias add, and the
+// backward recomputes that pre-activation instead of reading it back.
+// `cols` (a multiple of 8) is the row width, so an 8-value chunk never
+// straddles two rows.
+template <bool kBias>
+__global__ void bias_gelu_fwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ bias, bf16* __restrict__ y,
+                                     int64_t n, int cols) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;
+  bf16x8 v = *reinterpret_cast<const bf16x8*>(x + i);
+  if (kBias) {
+    const bf16x8 b = *reinterpret_cast<const bf16x8*>(bias + i % cols);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] + (float)b[j]);
+  }
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = (bf16)gelu_f((float)v[j]);
+  *reinterpret_cast<bf16x8*>(y + i) = o;
+}
+
+__global__ void bias_gelu_bwd_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x,
+                                     const bf16* __restrict__ bias, bf16* __restrict__ dx, int64_t n, int cols) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;
+  bf16x8 v = *reinterpret_cast<const bf16x8*>(x + i);
+  const bf16x8 b = *reinterpret_cast<const bf16x8*>(bias + i % cols);
+  const bf16x8 g = *reinterpret_cast<const bf16x8*>(dy + i);
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float h = (float)(bf16)((float)v[j] + (float)b[j]);
+    o[j] = (bf16)((float)g[j] * gelu_grad_f(h));
+  }
+  *reinterpret_cast<bf16x8*>(dx + i) = o;
+}
+
 __global__ void gelu_fwd_kernel(const bf16* __restrict__ x, bf16* __restrict__ y, int64_t n) {
   int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (i + 8 <= n) {
@@ -336,20 +379,34 @@ __global__ void rope_table_kernel(bf16* __restrict__ cs, bf16* __restrict__ sn, 
   sn[idx] = (bf16)sinf(angle);
 }
 
-template <bool kBackward>
+// kBias: columns [0, cols) of each row first get bf16(x + bias[column]) (the
+// bias add of the linear that produced the rows, rig/nn.py:55-56), and only
+// the first heads * head_dim of them are then rotated: the q / k / v rows of
+// the fused projection in one pass.  Without it cols = heads * head_dim.
+template <bool kBackward, bool kBias = false>
 __global__ void rope_kernel(bf16* __restrict__ x, int64_t row_stride, int rows, int seq, int heads, int head_dim,
-                            const bf16* __restrict__ cs, const bf16* __restrict__ sn) {
+                            const bf16* __restrict__ cs, const bf16* __restrict__ sn,
+                            const bf16* __restrict__ bias = nullptr, int cols = 0) {
   const int half = head_dim / 2;
-  const int quads_per_row = heads * half / 4;  // 4 pairs (8 values) per thread
+  const int rotated = heads * head_dim;
+  const int chunks_per_row = (kBias ? cols : rotated) / 8;  // 4 pairs (8 values) per thread
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (int64_t)rows * quads_per_row) return;
-  int row = (int)(t / quads_per_row);
-  int q = (int)(t % quads_per_row);
-  int pair0 = q * 4;  // pair index within the row's rotated region
-  int h = pair0 / half, i0 = pair0 % half;
-  int pos = row % seq;
-  bf16* p = x + (size_t)row * row_stride + (size_t)h * head_dim + 2 * i0;
+  if (t >= (int64_t)rows * chunks_per_row) return;
+  int row = (int)(t / chunks_per_row);
+  const int c0 = 8 * (int)(t % chunks_per_row);  // first column of the chunk
+  bf16* p = x + (size_t)row * row_stride + c0;
   bf16x8 v = *reinterpret_cast<bf16x8*>(p);
+  if (kBias) {
+    const bf16x8 b = *reinterpret_cast<const bf16x8*>(bias + c0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] + (float)b[j]);
+    if (c0 >= rotated) {
+      *reinterpret_cast<bf16x8*>(p) = v;
+      return;
+    }
+  }
+  const int i0 = (c0 % head_dim) / 2;  // pairs are (even, odd) columns of a head
+  int pos = row % seq;
   bf16x4 c4 = *reinterpret_cast<const bf16x4*>(cs + (size_t)pos * half + i0);
   bf16x4 s4 = *reinterpret_cast<const bf16x4*>(sn + (size_t)pos * half + i0);
   bf16x8 o;
@@ -599,22 +656,29 @@ int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, i
   if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
   if (rows == 0) return GPTRIG_OK;
   rmsnorm_fwd_kernel<false><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
-      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, nullptr, 1.0f, nullptr);
+      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, nullptr, 1.0f, nullptr, nullptr);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_add_bias_rmsnorm_fwd(const void* x, const void* branch, const void* branch_bias, float branch_scale,
+                                const void* scale, void* sum, void* y, float* rstd, int rows, int d, void* stream) {
+  if (!x || !branch || !scale || !sum || !y) return GPTRIG_E_NULL;
+  if (rows < 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
+  if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
+  if (y == x || y == sum || y == branch || sum == branch) return GPTRIG_E_SHAPE;
+  if ((uintptr_t)branch_bias & 7) return GPTRIG_E_SHAPE;  // 8-byte vector reads
+  if (rows == 0) return GPTRIG_OK;
+  rmsnorm_fwd_kernel<true><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, (const bf16*)branch, branch_scale, (bf16*)sum,
+      (const bf16*)branch_bias);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
 
 int gptrig_add_rmsnorm_fwd(const void* x, const void* branch, float branch_scale, const void* scale, void* sum,
                            void* y, float* rstd, int rows, int d, void* stream) {
-  if (!x || !branch || !scale || !sum || !y) return GPTRIG_E_NULL;
-  if (rows < 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
-  if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
-  if (y == x || y == sum || y == branch || sum == branch) return GPTRIG_E_SHAPE;
-  if (rows == 0) return GPTRIG_OK;
-  rmsnorm_fwd_kernel<true><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
-      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, (const bf16*)branch, branch_scale, (bf16*)sum);
-  GPTRIG_CHECK_LAUNCH();
-  return GPTRIG_OK;
+  return gptrig_add_bias_rmsnorm_fwd(x, branch, nullptr, branch_scale, scale, sum, y, rstd, rows, d, stream);
 }
 
 static int rmsnorm_bwd_blocks(int rows) {
@@ -702,6 +766,31 @@ int gptrig_gelu_bwd(const void* dy, const void* x, void* dx, int64_t n, void* st
   return GPTRIG_OK;
 }
 
+int gptrig_bias_gelu_fwd(const void* x, const void* bias, void* y, int rows, int cols, void* stream) {
+  if (!x || !bias || !y) return GPTRIG_E_NULL;
+  if (rows < 0 || cols <= 0 || cols % 8) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)x | (uintptr_t)bias | (uintptr_t)y) & 15) return GPTRIG_E_SHAPE;  // 16-byte vector accesses
+  if (rows == 0) return GPTRIG_OK;
+  const int64_t n = (int64_t)rows * cols;
+  bias_gelu_fwd_kernel<true><<<ceil_div(n / 8, 256), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)x, (const bf16*)bias, (bf16*)y, n, cols);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
+int gptrig_bias_gelu_bwd(const void* dy, const void* x, const void* bias, void* dx, int rows, int cols,
+                         void* stream) {
+  if (!dy || !x || !bias || !dx) return GPTRIG_E_NULL;
+  if (rows < 0 || cols <= 0 || cols % 8) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)dy | (uintptr_t)x | (uintptr_t)bias | (uintptr_t)dx) & 15) return GPTRIG_E_SHAPE;
+  if (rows == 0) return GPTRIG_OK;
+  const int64_t n = (int64_t)rows * cols;
+  bias_gelu_bwd_kernel<<<ceil_div(n / 8, 256), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)dy, (const bf16*)x, (const bf16*)bias, (bf16*)dx, n, cols);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
+}
+
 int gptrig_rope_table(void* cos_table, void* sin_table, int seq, int head_dim, void* stream) {
   if (!cos_table || !sin_table) return GPTRIG_E_NULL;
   if (seq <= 0 || head_dim <= 0 || (head_dim & 1)) return GPTRIG_E_SHAPE;
@@ -732,6 +821,22 @@ static int rope_launch(bool backward, void* x, int64_t row_stride, int rows, int
 int gptrig_rope_fwd(void* x, int64_t row_stride, int rows, int seq, int heads, int head_dim, const void* cos_table,
                     const void* sin_table, void* stream) {
   return rope_launch(false, x, row_stride, rows, seq, heads, head_dim, cos_table, sin_table, stream);
+}
+
+int gptrig_bias_rope_fwd(void* x, int64_t row_stride, int rows, int cols, const void* bias, int seq, int heads,
+                         int head_dim, const void* cos_table, const void* sin_table, void* stream) {
+  if (!x || !bias || !cos_table || !sin_table) return GPTRIG_E_NULL;
+  if (rows < 0 || seq <= 0 || heads <= 0 || head_dim <= 0) return GPTRIG_E_SHAPE;
+  if (head_dim % 8 || cols % 8 || row_stride % 8 || cols < heads * head_dim || row_stride < cols)
+    return GPTRIG_E_SHAPE;
+  if (((uintptr_t)x | (uintptr_t)bias) & 15) return GPTRIG_E_SHAPE;  // 16-byte vector accesses
+  if (rows == 0) return GPTRIG_OK;
+  const long long threads = (long long)rows * (cols / 8);
+  rope_kernel<false, true><<<ceil_div(threads, 256), 256, 0, (hipStream_t)stream>>>(
+      (bf16*)x, row_stride, rows, seq, heads, head_dim, (const bf16*)cos_table, (const bf16*)sin_table,
+      (const bf16*)bias, cols);
+  GPTRIG_CHECK_LAUNCH();
+  return GPTRIG_OK;
 }
 
 int gptrig_rope_bwd(void* dx, int64_t row_stride, int rows, int seq, int heads, int head_dim,

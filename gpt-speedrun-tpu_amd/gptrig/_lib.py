@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_flce_bwd_keep": (I, [P, P, P, P, P, F, P, P, I, P, Z, P, Z, I, I, I, I, P]),
     "gptrig_rmsnorm_fwd": (I, [P, P, P, P, I, I, P]),
     "gptrig_add_rmsnorm_fwd": (I, [P, P, F, P, P, P, P, I, I, P]),
+    "gptrig_add_bias_rmsnorm_fwd": (I, [P, P, P, F, P, P, P, P, I, I, P]),
     "gptrig_rmsnorm_bwd_workspace_bytes": (Z, [I, I]),
     "gptrig_rmsnorm_bwd": (I, [P, P, P, P, P, P, P, I, P, Z, I, I, P]),
     "gptrig_bias_grad": (I, [P, I, I, P, P]),
@@ -50,9 +51,12 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_linear_dgelu": (I, [P, L, P, L, I, P, L, P, L, I, I, I, P]),
     "gptrig_gelu_fwd": (I, [P, P, L, P]),
     "gptrig_gelu_bwd": (I, [P, P, P, L, P]),
+    "gptrig_bias_gelu_fwd": (I, [P, P, P, I, I, P]),
+    "gptrig_bias_gelu_bwd": (I, [P, P, P, P, I, I, P]),
     "gptrig_rope_table": (I, [P, P, I, I, P]),
     "gptrig_rope_fwd": (I, [P, L, I, I, I, I, P, P, P]),
     "gptrig_rope_bwd": (I, [P, L, I, I, I, I, P, P, P]),
+    "gptrig_bias_rope_fwd": (I, [P, L, I, I, P, I, I, I, P, P, P]),
     "gptrig_embedding_fwd": (I, [P, P, P, I, I, I, P]),
     "gptrig_embedding_bwd": (I, [P, P, P, I, I, I, P]),
     "gptrig_adamw": (I, [P, P, P, P, P, P, P, L, I, F, F, F, I, P, P, P]),

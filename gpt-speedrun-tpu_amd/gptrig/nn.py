@@ -38,16 +38,22 @@ def rmsnorm_forward(x2: torch.Tensor, scale_bf16: torch.Tensor, out: torch.Tenso
 
 
 def add_rmsnorm_forward(x2: torch.Tensor, branch: torch.Tensor, branch_scale: float, scale_bf16: torch.Tensor,
-                        sum_out: torch.Tensor | None = None, out: torch.Tensor | None = None):
+                        sum_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                        branch_bias: torch.Tensor | None = None):
     """``s = x + bf16(branch * branch_scale)`` then ``rms_norm(s)``: the block's
-    residual add and the norm after it in one pass.  Returns ``(s, y, rstd)``."""
+    residual add and the norm after it in one pass.  Returns ``(s, y, rstd)``.
+
+    ``branch_bias`` (bf16 ``[d]``): ``branch`` is a linear's bf16 GEMM output
+    without its bias, which is added here with its own rounding
+    (``rig/nn.py:55-56``) before the residual add."""
 
     rows, d = x2.shape
     s = torch.empty_like(x2) if sum_out is None else sum_out
     y = torch.empty_like(x2) if out is None else out
     rstd = torch.empty(rows, dtype=torch.float32, device=x2.device)
-    _lib.call("gptrig_add_rmsnorm_fwd", x2.data_ptr(), branch.data_ptr(), float(branch_scale), scale_bf16.data_ptr(),
-              s.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, d, _lib.stream())
+    _lib.call("gptrig_add_bias_rmsnorm_fwd", x2.data_ptr(), branch.data_ptr(), _lib.ptr(branch_bias),
+              float(branch_scale), scale_bf16.data_ptr(), s.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, d,
+              _lib.stream())
     return s, y, rstd
 
 
@@ -112,6 +118,17 @@ def rope_inplace(buf: torch.Tensor, row_stride: int, rows: int, seq: int, heads:
     c, s = rope_tables(seq, head_dim, buf.device)
     _lib.call("gptrig_rope_bwd" if backward else "gptrig_rope_fwd", buf.data_ptr(), int(row_stride), rows, seq,
               heads, head_dim, c.data_ptr(), s.data_ptr(), _lib.stream())
+
+
+def bias_rope_inplace(buf: torch.Tensor, bias: torch.Tensor, seq: int, heads: int, head_dim: int) -> None:
+    """In place on a ``[rows, cols]`` bf16 projection output without its bias:
+    every column gets ``bf16(x + bias)`` (``rig/nn.py:55-56``), then the first
+    ``heads * head_dim`` columns are rotated (``rig/nn.py:36-52``)."""
+
+    rows, cols = buf.shape
+    c, s = rope_tables(seq, head_dim, buf.device)
+    _lib.call("gptrig_bias_rope_fwd", buf.data_ptr(), int(buf.stride(0)), rows, cols, bias.data_ptr(), seq, heads,
+              head_dim, c.data_ptr(), s.data_ptr(), _lib.stream())
 
 
 class _Rotary(torch.autograd.Function):

@@ -34,7 +34,7 @@ import torch
 from . import _lib
 from .attention import attention_softmax_scale, document_segments
 from .kernels import linear_cross_entropy as lce
-from .nn import add_rmsnorm_forward, normal, rmsnorm_backward, rmsnorm_forward, rope_inplace, rope_tables
+from .nn import add_rmsnorm_forward, bias_rope_inplace, normal, rmsnorm_backward, rmsnorm_forward, rope_tables
 from .optim import OptimizerConfig, effective_adam_betas, learning_rate, tensor_hparams
 
 BF16 = torch.bfloat16
@@ -414,33 +414,40 @@ class GPTTrainer:
             xf, rstdf = rmsnorm_forward(x, A.w("final_ln_scale"))
         else:
             xn1, rstd1 = rmsnorm_forward(x, A.w("blocks/0/ln1_scale"), out=lin_in[0]["qkv"])
+        # Each linear is the GEMM alone (bf16 output); its bias is added, with
+        # its own rounding as in rig/nn.py:55-56, by the pass that consumes it
+        # (the RoPE pass, the GELU, the residual add).
         for i in range(c.layers):
             p = f"blocks/{i}/"
-            qkv = torch.addmm(A.w(p + "qkv_b"), xn1, A.wt(p + "qkv_w").t())
-            rope_inplace(qkv, 3 * d, N, S, 2 * H, D)
+            qkv = torch.mm(xn1, A.wt(p + "qkv_w").t())
+            bias_rope_inplace(qkv, A.w(p + "qkv_b"), S, 2 * H, D)
             o = lin_in[i]["attn"]
             lse = torch.empty((Bm, H, S), dtype=F32, device=self.device)
             with self._timed("attn_fwd"):
                 _lib.call("gptrig_attn_fwd", qkv.data_ptr(), qkv[:, d:].data_ptr(), qkv[:, 2 * d:].data_ptr(),
                           _lib.ptr(seg), o.data_ptr(), lse.data_ptr(), Bm, H, S, D, attn_strides.data_ptr(),
                           self.scale, stream)
-            x1, xn2, rstd2 = add_rmsnorm_forward(x, torch.addmm(A.w(p + "attn_b"), o, A.wt(p + "attn_w").t()),
+            x1, xn2, rstd2 = add_rmsnorm_forward(x, torch.mm(o, A.wt(p + "attn_w").t()),
                                                  self.residual_scale, A.w(p + "ln2_scale"),
-                                                 out=None if c.experts else lin_in[i]["mlp_up"])
+                                                 out=None if c.experts else lin_in[i]["mlp_up"],
+                                                 branch_bias=A.w(p + "attn_b"))
             if c.experts:
                 down, mlp_state = self._routed_forward(p, xn2)
             else:
-                h = torch.addmm(A.w(p + "mlp_up_b"), xn2, A.wt(p + "mlp_up_w").t())
+                h = torch.mm(xn2, A.wt(p + "mlp_up_w").t())  # the pre-activation before its bias
                 g = lin_in[i]["mlp_down"]
-                _lib.call("gptrig_gelu_fwd", h.data_ptr(), g.data_ptr(), h.numel(), stream)
-                down = torch.addmm(A.w(p + "mlp_down_b"), g, A.wt(p + "mlp_down_w").t())
+                _lib.call("gptrig_bias_gelu_fwd", h.data_ptr(), A.w(p + "mlp_up_b").data_ptr(), g.data_ptr(),
+                          h.shape[0], h.shape[1], stream)
+                down = torch.mm(g, A.wt(p + "mlp_down_w").t())
                 mlp_state = (h, g)
+            down_b = None if c.experts else A.w(p + "mlp_down_b")
             if i + 1 < c.layers:
                 x2, xn1_next, rstd1_next = add_rmsnorm_forward(x1, down, self.residual_scale,
                                                                A.w(f"blocks/{i + 1}/ln1_scale"),
-                                                               out=lin_in[i + 1]["qkv"])
+                                                               out=lin_in[i + 1]["qkv"], branch_bias=down_b)
             else:
-                x2, xf, rstdf = add_rmsnorm_forward(x1, down, self.residual_scale, A.w("final_ln_scale"))
+                x2, xf, rstdf = add_rmsnorm_forward(x1, down, self.residual_scale, A.w("final_ln_scale"),
+                                                    branch_bias=down_b)
             saved.append((x, xn1, rstd1, qkv, o, lse, x1, xn2, rstd2, mlp_state))
             x = x2
             if i + 1 < c.layers:
@@ -533,7 +540,8 @@ class GPTTrainer:
                 h, _ = mlp_state
                 dg = torch.mm(dm, A.w(p + "mlp_down_w").t())
                 dh = lin_dout[i]["mlp_up"]
-                _lib.call("gptrig_gelu_bwd", dg.data_ptr(), h.data_ptr(), dh.data_ptr(), dh.numel(), stream)
+                _lib.call("gptrig_bias_gelu_bwd", dg.data_ptr(), h.data_ptr(), A.w(p + "mlp_up_b").data_ptr(),
+                          dh.data_ptr(), dh.shape[0], dh.shape[1], stream)
                 dxn2 = torch.mm(dh, A.w(p + "mlp_up_w").t())
             dx1, _ = rmsnorm_backward(dxn2, x1, A.w(p + "ln2_scale"), rstd2, A.grad(p + "ln2_scale"), True,
                                       dresidual=dx, out=lin_dout[i]["attn"] if unit else None)

@@ -161,6 +161,13 @@ int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, i
  * sum may be x (in place); y must not alias x, branch or sum. */
 int gptrig_add_rmsnorm_fwd(const void* x, const void* branch, float branch_scale, const void* scale, void* sum,
                            void* y, float* rstd, int rows, int d, void* stream);
+/* The same with the bias add of the linear that produced branch done here:
+ * rig/nn.py:55-56 rounds the GEMM output to bf16 and then adds
+ * b.astype(bf16) with a second rounding, so branch (the bf16 GEMM output
+ * without bias) becomes bf16(branch + branch_bias[column]) before the
+ * residual add.  branch_bias bf16 [d] (8-byte aligned), or NULL for none. */
+int gptrig_add_bias_rmsnorm_fwd(const void* x, const void* branch, const void* branch_bias, float branch_scale,
+                                const void* scale, void* sum, void* y, float* rstd, int rows, int d, void* stream);
 size_t gptrig_rmsnorm_bwd_workspace_bytes(int rows, int d);
 /* dx bf16 = d rms_norm/dx (+ dresidual if non-NULL); dscale f32 [d] (+= if accumulate). */
 int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const float* rstd, const void* dresidual,
@@ -215,6 +222,15 @@ int gptrig_linear_dgelu(const void* dy, int64_t lddy, const void* w, int64_t ldw
  * recipes/reference/train.py:1171.  bf16 [n]. */
 int gptrig_gelu_fwd(const void* x, void* y, int64_t n, void* stream);
 int gptrig_gelu_bwd(const void* dy, const void* x, void* dx, int64_t n, void* stream);
+/* The same after the up-projection's bias add (rig/nn.py:55-56, the GEMM
+ * output rounded to bf16, then + b.astype(bf16) rounded again,
+ * recipes/reference/train.py:1170-1171): x bf16 [rows, cols] is the GEMM
+ * output without bias, bias bf16 [cols]; y = bf16(gelu(bf16(x + bias))) and
+ * dx = bf16(dy * gelu'(bf16(x + bias))).  cols a multiple of 8, every
+ * pointer 16-byte aligned. */
+int gptrig_bias_gelu_fwd(const void* x, const void* bias, void* y, int rows, int cols, void* stream);
+int gptrig_bias_gelu_bwd(const void* dy, const void* x, const void* bias, void* dx, int rows, int cols,
+                         void* stream);
 
 /* Interleaved RoPE, base 10000: rig/nn.py:36-52 (apply_rotary).
  * rope_table fills bf16 cos/sin [seq, head_dim/2].  rope_fwd/bwd rotate, in
@@ -225,6 +241,15 @@ int gptrig_rope_fwd(void* x, int64_t row_stride, int rows, int seq, int heads, i
                     const void* sin_table, void* stream);
 int gptrig_rope_bwd(void* dx, int64_t row_stride, int rows, int seq, int heads, int head_dim,
                     const void* cos_table, const void* sin_table, void* stream);
+/* The fused projection's bias add and the RoPE of its q / k columns in one
+ * in-place pass (rig/nn.py:55-56 then :36-52, recipes/reference/train.py:
+ * 1136-1142): columns [0, cols) of each row become bf16(x + bias[column]),
+ * the rounding of the linear's bias add after its bf16 GEMM output, and the
+ * first heads * head_dim of them are then rotated as gptrig_rope_fwd does.
+ * cols, head_dim and row_stride multiples of 8, heads * head_dim <= cols <=
+ * row_stride; x and bias 16-byte aligned. */
+int gptrig_bias_rope_fwd(void* x, int64_t row_stride, int rows, int cols, const void* bias, int seq, int heads,
+                         int head_dim, const void* cos_table, const void* sin_table, void* stream);
 
 /* Token-embedding gather (recipes/reference/train.py:1107) and its transpose:
  * out bf16 [n, d] = table[tokens]; dtable f32 [vocab, d] += scatter(dout). */

@@ -14,7 +14,11 @@ Pinning (what keeps a mistake in this restatement from passing silently):
 
 * attention fwd   - brute-force per-row softmax loops (tests/test_oracle_attention.py),
                     causal-prefix invariance, document independence,
-                    single-segment equivalence, padding transparency.
+                    single-segment equivalence, padding transparency; the
+                    kernel-numerics forward: the exact float64 softmax when
+                    its probabilities are left unrounded (every tile shape,
+                    padding, block skipping, documents), the one-chunk closed
+                    form with bf16 probabilities, the reference's tile choice.
 * attention bwd   - float64 torch autograd of the dense softmax formula
                     (an independent derivation of the same gradient).
 * FLCE fwd/bwd    - dense log-softmax + autograd; storage-row zero grads;

@@ -10,10 +10,17 @@ windows) except for one of:
   reference fixes the result only up to the accumulation order of its dots);
 * ``dense_attention``: the reference's own dense attention backend
   (``recipes/reference/train.py:1151-1162``: QK^T rounded to bf16, mask
-  ``finfo(f32).min``) instead of the flash kernels' semantics
-  (``rig/kernels/tpu_flash_attention.py:171-207``).
+  ``finfo(f32).min``; the backend its train.py runs off TPU) instead of the
+  Pallas kernel's numerics (``rig/kernels/tpu_flash_attention.py:236-349``);
+* ``normalized_attention``: the attention forward of the kernel's test
+  oracle (``tpu_flash_attention.py:171-207``: the normalised softmax rounded
+  to bf16 before the PV product) instead of the kernel's (the unnormalised
+  ``exp(s - running max)`` rounded per 256-key chunk).
 
-Usage: ``python tests/golden/make_trajectory_perturbed.py f64_linear|dense_attention``
+* ``eight_threads``: nothing but the CPU thread count (8 instead of the
+  fixture's 3), which changes torch's float32 summation order.
+
+Usage: ``python tests/golden/make_trajectory_perturbed.py f64_linear|dense_attention|normalized_attention|eight_threads``
 (10-40 minutes on 8 cores).  Output:
 ``tests/golden/config_a_trajectory_<variation>.json``.
 """
@@ -31,10 +38,12 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 import torch  # noqa: E402
 
+from oracle import attention as oattn  # noqa: E402
 from oracle import model as om  # noqa: E402
 
 STEPS = 20
 SEED = 0
+THREADS = 3  # as make_trajectory.py
 
 
 def linear_f64(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -47,14 +56,23 @@ def linear_f64(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, dtype:
 
 def main() -> None:
     variation = sys.argv[1] if len(sys.argv) > 1 else "f64_linear"
-    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(8 if variation == "eight_threads" else THREADS)
     config = om.baseline_config("A", steps=STEPS)
     if variation == "f64_linear":
         om.linear = linear_f64
         note = "dense linears accumulate in float64 instead of float32"
     elif variation == "dense_attention":
         config = replace(config, attention_backend="dense")
-        note = "the reference's dense attention backend (train.py:1151-1162) instead of the flash semantics"
+        note = "the reference's dense attention backend (train.py:1151-1162) instead of the flash kernel's numerics"
+    elif variation == "eight_threads":
+        note = "the same computation on 8 CPU threads instead of 3 (float32 summation order)"
+    elif variation == "normalized_attention":
+        def normalized(q, k, v, *, softmax_scale=None, segment_ids=None):
+            return oattn.attention_forward(q, k, v, softmax_scale=softmax_scale, segment_ids=segment_ids)
+
+        oattn.flash_attention_forward = normalized
+        note = ("the kernel's test-oracle attention forward (tpu_flash_attention.py:171-207, normalised "
+                "probabilities rounded) instead of the kernel's own (:236-349)")
     else:
         raise SystemExit(f"unknown variation {variation!r}")
     windows = om.synthetic_windows(SEED, STEPS, config.batch_size, config.seq_len, config.vocab_size)

@@ -42,22 +42,51 @@ def test_fixture_first_loss_is_near_uniform():
     assert abs(rows[0, 0] - math.log(50304)) <= 0.02 * math.log(50304)
 
 
+# Largest per-step loss difference from the fixture that each variation was
+# measured at (tests/golden/make_trajectory_perturbed.py), with a margin.
+SEMANTIC_BOUNDS = {  # measured 0.10%, 0.14%, 0.15%, all at step 8
+    "f64_linear": 3e-3,
+    "normalized_attention": 3e-3,
+    "dense_attention": 3e-3,
+}
+THREADS_BOUND = 1.5e-2  # measured 1.22% at step 8
+
+
+def check_variation(variation, bound, base):
+    path = os.path.join(os.path.dirname(__file__), "golden", f"config_a_trajectory_{variation}.json")
+    with open(path) as f:
+        rows = np.asarray(json.load(f)["rows"], dtype=np.float64)
+    loss_rel = np.abs(rows[:, 0] - base[:, 0]) / base[:, 0]
+    assert float(loss_rel.max()) <= bound, (variation, loss_rel)
+    assert float(loss_rel.max()) > 0.0, variation  # the variation does change the run
+    assert float(loss_rel[:5].max()) <= 5e-4, variation  # before the loss spike
+    np.testing.assert_allclose(rows[:, 1], base[:, 1], rtol=1e-7)
+    assert float(np.abs(rows[0, 2] - base[0, 2]) / base[0, 2]) <= 5e-3, variation
+    return float(loss_rel.max())
+
+
 def test_equivalent_restatements_stay_within_the_trajectory_gate():
     """The basis of the GPU trajectory gate: the oracle's 20-step run redone
-    with a variation the reference itself treats as the same computation
-    (``tests/golden/make_trajectory_perturbed.py``: its dense attention backend,
-    ``recipes/reference/train.py:1151-1162``, or float64 accumulation in the
-    linears) stays within 0.3% of the fixture's loss on every step (the gate is
-    1%), with identical learning rates and identical first-step gradient norms
-    to 0.5%, while single-step gradient norms may differ by up to ~10%."""
+    with a change the reference itself treats as the same computation --
+    float64 accumulation in the linears, or the attention forward of the
+    kernel's test oracle (normalised probabilities rounded) or of the
+    reference's dense backend (``recipes/reference/train.py:1151-1162``)
+    instead of the Pallas kernel's numerics -- stays within 0.3% of the
+    fixture's loss on every step (the gate is 1%), with identical learning
+    rates and first-step gradient norms to 0.5%; single-step gradient norms
+    differ by up to 5% (and the dense backend's by 4x at step 20)."""
     with open(FIXTURE) as f:
         base = np.asarray(json.load(f)["rows"], dtype=np.float64)
-    for variation in ("dense_attention", "f64_linear"):
-        path = os.path.join(os.path.dirname(__file__), "golden", f"config_a_trajectory_{variation}.json")
-        with open(path) as f:
-            rows = np.asarray(json.load(f)["rows"], dtype=np.float64)
-        loss_rel = np.abs(rows[:, 0] - base[:, 0]) / base[:, 0]
-        assert float(loss_rel.max()) <= 3e-3, (variation, loss_rel)
-        assert float(loss_rel.max()) > 0.0, variation  # the variation does change the run
-        np.testing.assert_allclose(rows[:, 1], base[:, 1], rtol=1e-7)
-        assert float(np.abs(rows[0, 2] - base[0, 2]) / base[0, 2]) <= 5e-3, variation
+    for variation, bound in SEMANTIC_BOUNDS.items():
+        check_variation(variation, bound, base)
+
+
+def test_summation_order_alone_moves_the_loss_spike():
+    """The same oracle on 8 CPU threads instead of the fixture's 3 (only the
+    float32 summation order changes) follows the fixture to 0.05% through
+    step 5 and then departs by up to 1.2% at step 8: around its loss spike
+    (steps 4-9) this run is chaotic, so the 1% gate is tight there for any
+    implementation whose reductions add in another order."""
+    with open(FIXTURE) as f:
+        base = np.asarray(json.load(f)["rows"], dtype=np.float64)
+    assert check_variation("eight_threads", THREADS_BOUND, base) > 5e-3

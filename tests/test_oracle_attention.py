@@ -1,9 +1,12 @@
 """Pins ``oracle.attention`` (CPU only).
 
-Forward: brute-force per-row softmax in pure Python.  Backward: float64
-autograd of the textbook softmax-attention formula (an independent
-derivation).  Invariants mirror ``tests/test_tpu_flash_attention.py`` of the
-reference (causal prefix ``:34-39``, documents ``:107-136``).
+Forward: brute-force per-row softmax in pure Python; the kernel-numerics
+forward against the exact softmax with unrounded probabilities (every tile
+shape, padding and block skipping) and, with bf16 probabilities, against the
+one-chunk closed form ``sum_j bf16(exp(s_j - m)) v_j / sum_j exp(s_j - m)``.
+Backward: float64 autograd of the textbook softmax-attention formula (an
+independent derivation).  Invariants mirror ``tests/test_tpu_flash_attention.py``
+of the reference (causal prefix ``:34-39``, documents ``:107-136``).
 """
 
 from __future__ import annotations
@@ -136,3 +139,69 @@ def test_validation_errors():
         oa.reference_causal_attention(*qkv((1, 1, 8, 12)))
     with pytest.raises(TypeError):
         oa.reference_causal_attention(q, k.double(), v)
+
+
+def test_flash_tiles_follow_the_reference_choice():
+    # select_attention_tiles (tpu_flash_attention.py:112-142): 512/512/256 is
+    # the preferred shape and legal from S = 512 on; shorter or odd extents fall
+    # back to the nearest legal candidate.
+    assert oa.flash_tiles(1024) == (512, 512, 256)
+    assert oa.flash_tiles(2048) == (512, 512, 256)
+    assert oa.flash_tiles(512) == (512, 512, 256)
+    assert oa.flash_tiles(256) == (256, 256, 128)
+    assert oa.flash_tiles(200) == (256, 256, 128)  # padded to 256
+    assert oa.flash_tiles(384) == (128, 128, 128)
+    assert oa.flash_tiles(100) == (128, 128, 128)
+
+
+def bf16_ulps(a, b):
+    ai = a.to(torch.bfloat16).view(torch.int16).int()
+    bi = b.to(torch.bfloat16).view(torch.int16).int()
+    return (ai - bi).abs()
+
+
+@pytest.mark.parametrize("S,segmented", [(9, False), (200, False), (300, True), (1024, False), (1024, True)])
+def test_flash_forward_with_unrounded_probabilities_is_the_exact_softmax(S, segmented):
+    # With float32 probabilities the rescaled recurrence is the exact softmax
+    # average whatever the tiles: this pins the chunk order, the running max,
+    # the corrections, the block skipping, the padding mask and the LSE.
+    g = torch.Generator().manual_seed(S)
+    q, k, v = ((torch.randn((1, 2, S, 16), generator=g) * 0.9).to(torch.bfloat16) for _ in range(3))
+    seg = segments_from_cuts(S, (0, S // 3, S // 3 + 1, (2 * S) // 3)) if segmented else None
+    o, lse = oa.flash_attention_forward(q, k, v, softmax_scale=0.4, segment_ids=seg, probability_dtype=torch.float32)
+    s = (q.double() @ k.double().transpose(-1, -2)) * 0.4
+    s = s.masked_fill(~oa.visibility(S, seg), float("-inf"))
+    want = torch.softmax(s, -1) @ v.double()
+    ulps = bf16_ulps(o, want)
+    assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) < 0.02
+    np.testing.assert_allclose(lse.double().numpy(), torch.logsumexp(s, -1).numpy(), rtol=2e-6, atol=2e-6)
+
+
+def test_flash_forward_rounds_the_unnormalised_probabilities():
+    # S <= 128 is one chunk: out = sum_j bf16(e_j) v_j / sum_j e_j with
+    # e_j = exp(s_j - max_j s_j), the normaliser taken from the unrounded e.
+    q, k, v = qkv((1, 1, 40, 8), seed=11, scale=1.5, dtype=torch.bfloat16)
+    o, _ = oa.flash_attention_forward(q, k, v, softmax_scale=0.7)
+    want = np.zeros((40, 8))
+    for i in range(40):
+        s = [0.7 * float((q[0, 0, i].double() * k[0, 0, j].double()).sum()) for j in range(i + 1)]
+        m = max(s)
+        e = [math.exp(x - m) for x in s]
+        eb = [float(torch.tensor(x, dtype=torch.float32).to(torch.bfloat16)) for x in e]
+        for d in range(8):
+            want[i, d] = sum(eb[j] * float(v[0, 0, j, d]) for j in range(i + 1)) / sum(e)
+    ulps = bf16_ulps(o[0, 0].float(), torch.from_numpy(want))
+    assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) < 0.02
+    # ... which is not the normalised rounding of the kernel's test oracle.
+    assert not torch.equal(o, oa.reference_causal_attention(q, k, v, softmax_scale=0.7))
+
+
+def test_flash_forward_rows_inside_the_first_chunk_ignore_the_rest():
+    # Rows 0..255 of S = 1024 see only the first 256-key chunk: the later
+    # chunks of their block are fully masked (p = 0, correction 1), so they get
+    # the one-chunk result of the same rows computed alone.
+    q, k, v = qkv((1, 2, 1024, 16), seed=12, scale=1.0, dtype=torch.bfloat16)
+    full, lse_full = oa.flash_attention_forward(q, k, v)
+    alone, lse_alone = oa.flash_attention_forward(q[:, :, :128], k[:, :, :128], v[:, :, :128])
+    assert int(bf16_ulps(full[:, :, :128], alone).max()) <= 1
+    np.testing.assert_allclose(lse_full[:, :, :128].numpy(), lse_alone.numpy(), rtol=1e-6, atol=1e-6)
