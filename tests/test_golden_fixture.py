@@ -84,9 +84,10 @@ def test_equivalent_restatements_stay_within_the_trajectory_gate():
 def test_summation_order_alone_moves_the_loss_spike():
     """The same oracle on 8 CPU threads instead of the fixture's 3 (only the
     float32 summation order changes) follows the fixture to 0.05% through
-    step 5 and then departs by up to 1.2% at step 8: around its loss spike
-    (steps 4-9) this run is chaotic, so the 1% gate is tight there for any
-    implementation whose reductions add in another order."""
+    step 5 and then departs by 1.2% at step 8, outside the north star's 1%
+    gate: around its loss spike (steps 4-9) this run is chaotic, so the gate
+    is tight there for any implementation whose reductions add in another
+    order, the reference's own included."""
     with open(FIXTURE) as f:
         base = np.asarray(json.load(f)["rows"], dtype=np.float64)
-    assert check_variation("eight_threads", THREADS_BOUND, base) > 5e-3
+    assert check_variation("eight_threads", THREADS_BOUND, base) > 1e-2
