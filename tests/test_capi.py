@@ -62,6 +62,17 @@ def test_host_validation_rejects_bad_arguments_without_launching():
                             None) == -2
     # routing: too many experts
     assert lib.gptrig_moe_route(dummy, None, dummy, dummy, dummy, dummy, dummy, None, None, 0, 8, 65, 2, None) == -4
+    # bias-fused passes: misaligned bias / data, cols not a multiple of 8, v columns past the row stride
+    odd = ctypes.c_void_p(18)
+    assert lib.gptrig_bias_gelu_fwd(dummy, odd, dummy, 4, 64, None) == -2
+    assert lib.gptrig_bias_gelu_fwd(dummy, dummy, dummy, 4, 60, None) == -2
+    assert lib.gptrig_bias_gelu_bwd(dummy, odd, dummy, dummy, 4, 64, None) == -2
+    assert lib.gptrig_bias_gelu_fwd(None, dummy, dummy, 4, 64, None) == -1
+    assert lib.gptrig_bias_rope_fwd(dummy, 192, 4, 192, odd, 8, 2, 64, dummy, dummy, None) == -2
+    assert lib.gptrig_bias_rope_fwd(dummy, 128, 4, 192, dummy, 8, 2, 64, dummy, dummy, None) == -2
+    assert lib.gptrig_bias_rope_fwd(dummy, 192, 4, 96, dummy, 8, 2, 64, dummy, dummy, None) == -2
+    assert lib.gptrig_add_bias_rmsnorm_fwd(dummy, ctypes.c_void_p(32), ctypes.c_void_p(20), ctypes.c_float(1.0),
+                                           dummy, ctypes.c_void_p(48), ctypes.c_void_p(64), None, 4, 64, None) == -2
 
 
 def test_workspace_queries_are_bounded_by_the_chunk():
