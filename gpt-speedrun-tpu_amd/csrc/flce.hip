@@ -215,19 +215,45 @@ __global__ void __launch_bounds__(256) flce_target_logit_kernel(const bf16* __re
 
 // lse[n] (natural log) from the per-tile partials; loss = lse - target logit,
 // +inf for an invalid target (:159-172).
-__global__ void flce_combine_kernel(const float2* __restrict__ partial, int ntiles, int N, int sem_v,
-                                    const int32_t* __restrict__ targets, const float* __restrict__ tlogit,
-                                    float* __restrict__ lse, float* __restrict__ losses) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+// One (max, sum) pair folded into another (log2 domain); empty pairs (max
+// -inf, tiles past the semantic vocabulary) are skipped.
+__device__ __forceinline__ void lse_fold(float& m, float& s, float pm, float ps) {
+  if (pm == -INFINITY) return;
+  const float m2 = fmaxf(m, pm);
+  s = s * fast_exp2(m - m2) + ps * fast_exp2(pm - m2);
+  m = m2;
+}
+
+// 64 tokens per workgroup (lane = token), each of the 4 waves folding every
+// fourth tile, the 4 partial pairs then folded through LDS: 16 waves per CU
+// with independent loads instead of one serial chain per token.
+constexpr int kCombineWaves = 4;
+__global__ void __launch_bounds__(64 * kCombineWaves)
+    flce_combine_kernel(const float2* __restrict__ partial, int ntiles, int N, int sem_v,
+                        const int32_t* __restrict__ targets, const float* __restrict__ tlogit,
+                        float* __restrict__ lse, float* __restrict__ losses) {
+  __shared__ float2 part_s[kCombineWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + lane;
   float m = -INFINITY, s = 0.f;
-  for (int t = 0; t < ntiles; ++t) {
-    const float2 p = partial[(size_t)t * N + n];
-    if (p.x == -INFINITY) continue;
-    const float m2 = fmaxf(m, p.x);
-    s = s * fast_exp2(m - m2) + p.y * fast_exp2(p.x - m2);
-    m = m2;
+  if (n < N) {
+    int t = wave;
+    for (; t + kCombineWaves < ntiles; t += 2 * kCombineWaves) {  // two loads in flight
+      const float2 p0 = partial[(size_t)t * N + n];
+      const float2 p1 = partial[(size_t)(t + kCombineWaves) * N + n];
+      lse_fold(m, s, p0.x, p0.y);
+      lse_fold(m, s, p1.x, p1.y);
+    }
+    if (t < ntiles) {
+      const float2 p0 = partial[(size_t)t * N + n];
+      lse_fold(m, s, p0.x, p0.y);
+    }
   }
+  part_s[wave][lane] = float2{m, s};
+  __syncthreads();
+  if (wave != 0 || n >= N) return;
+#pragma unroll
+  for (int w = 1; w < kCombineWaves; ++w) lse_fold(m, s, part_s[w][lane].x, part_s[w][lane].y);
   const float l = (m + __log2f(s)) * GPTRIG_LN2;
   lse[n] = l;
   const int t = targets[n];
@@ -765,16 +791,23 @@ size_t keep_gt_bytes(int n, int vocab) { return align256((size_t)vocab * ceil_di
 // Backward from the kept softmax, step 1: the per-(half tile, token) maxima m
 // become the factors a = exp2(m - lse log2(e)) ct of their probabilities (in
 // place), ct the token's cotangent (0 for an invalid target).
+// blockIdx.y = the half tile, 4 tokens per thread (N % 8 == 0 on this path,
+// so a group of 4 is wholly in or out and 16-byte aligned).
 __global__ void flce_keep_alpha_kernel(float* __restrict__ mh, int halves, int N, int sem_v,
                                        const int32_t* __restrict__ targets, const float* __restrict__ lse,
                                        const float* __restrict__ cot, float cot_scale) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)halves * N) return;
-  const int n = (int)(i % N);
-  const int t = targets[n];
-  const float ct = (t >= 0 && t < sem_v) ? (cot ? cot[n] : cot_scale) : 0.f;
-  const float m = mh[i];
-  mh[i] = m == -INFINITY ? 0.f : fast_exp2(m - lse[n] * GPTRIG_LOG2E) * ct;
+  const int n0 = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (n0 >= N) return;
+  float* row = mh + (size_t)blockIdx.y * N + n0;
+  const f32x4 m = *reinterpret_cast<const f32x4*>(row);
+  const i32x4_t t = *reinterpret_cast<const i32x4_t*>(targets + n0);  // (targets is checked 16-byte aligned)
+  f32x4 a;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // lse and cot: scalar reads, no alignment asked of the caller
+    const float ct = (t[j] >= 0 && t[j] < sem_v) ? (cot ? cot[n0 + j] : cot_scale) : 0.f;
+    a[j] = m[j] == -INFINITY ? 0.f : fast_exp2(m[j] - lse[n0 + j] * GPTRIG_LOG2E) * ct;
+  }
+  *reinterpret_cast<f32x4*>(row) = a;
 }
 
 // Step 2: G^T[v][n] = bf16(p a - [v == t] ct), zero for v >= semantic vocab
@@ -892,8 +925,8 @@ int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targe
   flce_target_logit_kernel<<<ceil_div(n, 4), 256, 0, s>>>((const bf16*)hidden, (const bf16*)weight, targets, n, d,
                                                            semantic_vocab, tlogit);
   GPTRIG_CHECK_LAUNCH();
-  flce_combine_kernel<<<ceil_div(n, 256), 256, 0, s>>>(partial, ntiles, n, semantic_vocab, targets, tlogit, lse,
-                                                        losses);
+  flce_combine_kernel<<<ceil_div(n, 64), 64 * kCombineWaves, 0, s>>>(partial, ntiles, n, semantic_vocab, targets,
+                                                                      tlogit, lse, losses);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
@@ -1067,8 +1100,8 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
     GPTRIG_CHECK_LAUNCH();
   }
   const int halves = 2 * ceil_div(vocab, BM);
-  flce_keep_alpha_kernel<<<ceil_div((int64_t)halves * n, 256), 256, 0, s>>>(alpha, halves, n, semantic_vocab, targets,
-                                                                            lse, cotangent, cotangent_scale);
+  flce_keep_alpha_kernel<<<dim3((unsigned)ceil_div(n / 4, 256), (unsigned)halves), 256, 0, s>>>(
+      alpha, halves, n, semantic_vocab, targets, lse, cotangent, cotangent_scale);
   GPTRIG_CHECK_LAUNCH();
   const dim3 rgrid((unsigned)ceil_div(vocab * 4, 256), (unsigned)ceil_div(n, 32));
   flce_keep_rescale_kernel<<<rgrid, 256, 0, s>>>(gt, alpha, n, vocab, semantic_vocab, targets, cotangent,
