@@ -415,8 +415,9 @@ class GPTTrainer:
         else:
             xn1, rstd1 = rmsnorm_forward(x, A.w("blocks/0/ln1_scale"), out=lin_in[0]["qkv"])
         # The QKV projection is this library's GEMM with the bias add and the
-        # RoPE of q and k in its epilogue (gptrig_linear_rope, 7% faster at
-        # config D than hipBLASLt plus the bias + RoPE pass).  The other
+        # RoPE of q and k in its epilogue (gptrig_linear_rope: 281 against
+        # 301 us at config D in isolation for hipBLASLt plus the bias + RoPE
+        # pass; the same step time either way).  The other
         # linears are hipBLASLt GEMMs alone (bf16 output), their bias added,
         # with its own rounding as in rig/nn.py:55-56, by the pass that
         # consumes them (the GELU, the residual add).
