@@ -77,6 +77,76 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const bf16* x, const b
   }
 }
 
+// The same for d % 8 == 0 with 16-byte accesses: chunk c (8 values) of a row
+// is lane c % 64's (c / 64)-th, C8 = ceil(d / 512) chunks per lane.
+template <bool kAdd, int C8>
+__global__ void __launch_bounds__(256) rmsnorm_fwd8_kernel(const bf16* x, const bf16* __restrict__ scale,
+                                                           bf16* __restrict__ y, float* __restrict__ rstd, int rows,
+                                                           int d, const bf16* __restrict__ branch, float branch_scale,
+                                                           bf16* sum_out, const bf16* __restrict__ branch_bias) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const bf16* xr = x + (size_t)row * d;
+  bf16* yr = y + (size_t)row * d;
+  const int chunks = d / 8;
+  bf16x8 xv[C8];
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < C8; ++t) {
+    const int c = lane + kWave * t;
+    if (c < chunks) {
+      xv[t] = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
+      if (kAdd) {
+        bf16x8 bv = *reinterpret_cast<const bf16x8*>(branch + (size_t)row * d + 8 * c);
+        if (branch_bias) {  // the linear's own bias add, rounded before the residual add
+          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(branch_bias + 8 * c);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) bv[j] = (bf16)((float)bv[j] + (float)bb[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[t][j] = (bf16)((float)xv[t][j] + (float)(bf16)((float)bv[j] * branch_scale));
+        *reinterpret_cast<bf16x8*>(sum_out + (size_t)row * d + 8 * c) = xv[t];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += (float)xv[t][j] * (float)xv[t][j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)d + 1.0e-5f);
+  if (lane == 0 && rstd) rstd[row] = r;
+#pragma unroll
+  for (int t = 0; t < C8; ++t) {
+    const int c = lane + kWave * t;
+    if (c < chunks) {
+      const bf16x8 sv = *reinterpret_cast<const bf16x8*>(scale + 8 * c);
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (bf16)((float)(bf16)((float)xv[t][j] * r) * (float)sv[j]);
+      *reinterpret_cast<bf16x8*>(yr + 8 * c) = o;
+    }
+  }
+}
+
+// Launch of the forward: the 16-byte form when every row, the scale and the
+// bias are 16-byte aligned and d <= 2048, else the 8-byte one.
+template <bool kAdd>
+static void launch_rmsnorm_fwd(const bf16* x, const bf16* scale, bf16* y, float* rstd, int rows, int d,
+                               const bf16* branch, float branch_scale, bf16* sum, const bf16* bias, hipStream_t s) {
+  const uintptr_t al = (uintptr_t)x | (uintptr_t)scale | (uintptr_t)y | (uintptr_t)branch | (uintptr_t)sum |
+                       (uintptr_t)bias;
+  const int c8 = ceil_div(d / 8, 64);
+  const dim3 grid(ceil_div(rows, 4));
+  if (d % 8 == 0 && (al & 15) == 0 && c8 <= 4) {
+    if (c8 == 1) rmsnorm_fwd8_kernel<kAdd, 1><<<grid, 256, 0, s>>>(x, scale, y, rstd, rows, d, branch, branch_scale, sum, bias);
+    else if (c8 == 2) rmsnorm_fwd8_kernel<kAdd, 2><<<grid, 256, 0, s>>>(x, scale, y, rstd, rows, d, branch, branch_scale, sum, bias);
+    else if (c8 == 3) rmsnorm_fwd8_kernel<kAdd, 3><<<grid, 256, 0, s>>>(x, scale, y, rstd, rows, d, branch, branch_scale, sum, bias);
+    else rmsnorm_fwd8_kernel<kAdd, 4><<<grid, 256, 0, s>>>(x, scale, y, rstd, rows, d, branch, branch_scale, sum, bias);
+  } else {
+    rmsnorm_fwd_kernel<kAdd><<<grid, 256, 0, s>>>(x, scale, y, rstd, rows, d, branch, branch_scale, sum, bias);
+  }
+}
+
 // Backward of rms_norm by the chain rule through the two roundings:
 //   dn = bf16(dy * scale)                       (cotangent of the bf16 product)
 //   dx = r*dn - (r^3/d) * x * sum_j(dn_j x_j)   (fp32), rounded to bf16
@@ -655,8 +725,8 @@ int gptrig_rmsnorm_fwd(const void* x, const void* scale, void* y, float* rstd, i
   if (rows < 0 || d <= 0 || d % 4) return GPTRIG_E_SHAPE;
   if (d > 4 * 64 * kMaxChunks) return GPTRIG_E_UNSUPPORTED;
   if (rows == 0) return GPTRIG_OK;
-  rmsnorm_fwd_kernel<false><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
-      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, nullptr, 1.0f, nullptr, nullptr);
+  launch_rmsnorm_fwd<false>((const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, nullptr, 1.0f, nullptr, nullptr,
+                            (hipStream_t)stream);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
@@ -669,9 +739,8 @@ int gptrig_add_bias_rmsnorm_fwd(const void* x, const void* branch, const void* b
   if (y == x || y == sum || y == branch || sum == branch) return GPTRIG_E_SHAPE;
   if ((uintptr_t)branch_bias & 7) return GPTRIG_E_SHAPE;  // 8-byte vector reads
   if (rows == 0) return GPTRIG_OK;
-  rmsnorm_fwd_kernel<true><<<ceil_div(rows, 4), 256, 0, (hipStream_t)stream>>>(
-      (const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, (const bf16*)branch, branch_scale, (bf16*)sum,
-      (const bf16*)branch_bias);
+  launch_rmsnorm_fwd<true>((const bf16*)x, (const bf16*)scale, (bf16*)y, rstd, rows, d, (const bf16*)branch,
+                           branch_scale, (bf16*)sum, (const bf16*)branch_bias, (hipStream_t)stream);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
