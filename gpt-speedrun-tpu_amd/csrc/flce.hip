@@ -813,7 +813,9 @@ __global__ void flce_keep_alpha_kernel(float* __restrict__ mh, int halves, int N
 // Step 2: G^T[v][n] = bf16(p a - [v == t] ct), zero for v >= semantic vocab
 // (K1's values, from the kept fp16 p instead of recomputed logits), in place:
 // blockIdx.y = the 32-token block, one thread per 8 tokens of one row,
-// consecutive threads on consecutive 16 bytes.
+// consecutive threads on consecutive 16 bytes.  Non-temporal load and store:
+// the 6.6 GB pass gains nothing from keeping its lines in the caches
+// (0.6% off the FLCE sequence at config D in a same-box A/B).
 __global__ void __launch_bounds__(256)
     flce_keep_rescale_kernel(bf16* __restrict__ gt, const float* __restrict__ alpha, int N, int V, int sem_v,
                              const int32_t* __restrict__ targets, const float* __restrict__ cot, float cot_scale) {
@@ -826,7 +828,7 @@ __global__ void __launch_bounds__(256)
   bf16* g = gt + ((size_t)blk * V + v) * 32 + 8 * c;
   bf16x8 o = bf16x8{};
   if (v < sem_v) {
-    const f16x8 p = *reinterpret_cast<const f16x8*>(g);
+    const f16x8 p = __builtin_bit_cast(f16x8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g)));
     const float* a = alpha + (size_t)(2 * (v >> 8) + ((v >> 7) & 1)) * N + n0;
     const f32x4 a0 = *reinterpret_cast<const f32x4*>(a);
     const f32x4 a1 = *reinterpret_cast<const f32x4*>(a + 4);
@@ -841,7 +843,7 @@ __global__ void __launch_bounds__(256)
       o[j] = (bf16)g8;
     }
   }
-  *reinterpret_cast<bf16x8*>(g) = o;
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(g));
 }
 
 }  // namespace
