@@ -422,7 +422,8 @@ __global__ void __launch_bounds__(gemm::THREADS)
 }
 
 // C (fp32, row-major [M][ldc]) = / += / atomic+= A B over K range of this split.
-// mode 0: store, 1: accumulate (read-modify-write), 2: atomic add.
+// mode 0: store, 1: accumulate (read-modify-write), 2: atomic add,
+// 3: C is bf16 (row-major [M][ldc] elements) and gets bf16(A B) (one split).
 // colsum (nullable): colsum[n] atomic+= sum over this split's
 // K range of B(k, n), computed from the B fragments already in registers and shared out
 // over the M tiles (the bias gradient of a linear layer, fused into its
@@ -466,7 +467,9 @@ __global__ void __launch_bounds__(gemm::THREADS)
         const int m = tm * BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
         if (m >= M) continue;
         float* dst = C + (int64_t)m * ldc + n;
-        if (mode == 2)
+        if (mode == 3)
+          reinterpret_cast<bf16*>(C)[(int64_t)m * ldc + n] = (bf16)acc[mb][nb][i];
+        else if (mode == 2)
           atomicAdd(dst, acc[mb][nb][i]);
         else
           *dst = mode ? *dst + acc[mb][nb][i] : acc[mb][nb][i];
@@ -1096,7 +1099,11 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
     GPTRIG_CHECK_LAUNCH();
   }
-  {
+  // dh in one split (every K = vocabulary slice in one workgroup, as at the
+  // bench shape) is written as bf16 by the GEMM itself: no fp32 accumulator
+  // to zero, no atomics, no conversion pass.
+  const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vocab, gemm::BK));
+  if (dh_split > 1) {
     const int64_t total = (int64_t)n * d;
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, total);
     GPTRIG_CHECK_LAUNCH();
@@ -1117,7 +1124,12 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
                                                                                       dweight, d, 2, nullptr);
   GPTRIG_CHECK_LAUNCH();
   Operand Agt{gt, n, vc}, Bw{Wp, d};
-  const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
+  if (dh_split == 1) {
+    gemm_f32_kernel<false, false><<<tiles_of(n, d), gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, 1, (float*)dhidden, d,
+                                                                            3, nullptr);
+    GPTRIG_CHECK_LAUNCH();
+    return GPTRIG_OK;
+  }
   gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
                                                                                       dh_acc, d, 2, nullptr);
   GPTRIG_CHECK_LAUNCH();
