@@ -422,8 +422,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
 }
 
 // C (fp32, row-major [M][ldc]) = / += / atomic+= A B over K range of this split.
-// mode 0: store, 1: accumulate (read-modify-write), 2: atomic add,
-// 3: C is bf16 (row-major [M][ldc] elements) and gets bf16(A B) (one split).
+// mode 0: store, 1: accumulate (read-modify-write), 2: atomic add.
 // colsum (nullable): colsum[n] atomic+= sum over this split's
 // K range of B(k, n), computed from the B fragments already in registers and shared out
 // over the M tiles (the bias gradient of a linear layer, fused into its
@@ -467,9 +466,7 @@ __global__ void __launch_bounds__(gemm::THREADS)
         const int m = tm * BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
         if (m >= M) continue;
         float* dst = C + (int64_t)m * ldc + n;
-        if (mode == 3)
-          reinterpret_cast<bf16*>(C)[(int64_t)m * ldc + n] = (bf16)acc[mb][nb][i];
-        else if (mode == 2)
+        if (mode == 2)
           atomicAdd(dst, acc[mb][nb][i]);
         else
           *dst = mode ? *dst + acc[mb][nb][i] : acc[mb][nb][i];
@@ -816,9 +813,7 @@ __global__ void flce_keep_alpha_kernel(float* __restrict__ mh, int halves, int N
 // Step 2: G^T[v][n] = bf16(p a - [v == t] ct), zero for v >= semantic vocab
 // (K1's values, from the kept fp16 p instead of recomputed logits), in place:
 // blockIdx.y = the 32-token block, one thread per 8 tokens of one row,
-// consecutive threads on consecutive 16 bytes.  Non-temporal load and store:
-// the 6.6 GB pass gains nothing from keeping its lines in the caches
-// (0.6% off the FLCE sequence at config D in a same-box A/B).
+// consecutive threads on consecutive 16 bytes.
 __global__ void __launch_bounds__(256)
     flce_keep_rescale_kernel(bf16* __restrict__ gt, const float* __restrict__ alpha, int N, int V, int sem_v,
                              const int32_t* __restrict__ targets, const float* __restrict__ cot, float cot_scale) {
@@ -831,7 +826,7 @@ __global__ void __launch_bounds__(256)
   bf16* g = gt + ((size_t)blk * V + v) * 32 + 8 * c;
   bf16x8 o = bf16x8{};
   if (v < sem_v) {
-    const f16x8 p = __builtin_bit_cast(f16x8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g)));
+    const f16x8 p = *reinterpret_cast<const f16x8*>(g);
     const float* a = alpha + (size_t)(2 * (v >> 8) + ((v >> 7) & 1)) * N + n0;
     const f32x4 a0 = *reinterpret_cast<const f32x4*>(a);
     const f32x4 a1 = *reinterpret_cast<const f32x4*>(a + 4);
@@ -846,7 +841,7 @@ __global__ void __launch_bounds__(256)
       o[j] = (bf16)g8;
     }
   }
-  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(g));
+  *reinterpret_cast<bf16x8*>(g) = o;
 }
 
 }  // namespace
@@ -1099,11 +1094,7 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
     GPTRIG_CHECK_LAUNCH();
   }
-  // dh in one split (every K = vocabulary slice in one workgroup, as at the
-  // bench shape) is written as bf16 by the GEMM itself: no fp32 accumulator
-  // to zero, no atomics, no conversion pass.
-  const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vocab, gemm::BK));
-  if (dh_split > 1) {
+  {
     const int64_t total = (int64_t)n * d;
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, total);
     GPTRIG_CHECK_LAUNCH();
@@ -1124,12 +1115,7 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
                                                                                       dweight, d, 2, nullptr);
   GPTRIG_CHECK_LAUNCH();
   Operand Agt{gt, n, vc}, Bw{Wp, d};
-  if (dh_split == 1) {
-    gemm_f32_kernel<false, false><<<tiles_of(n, d), gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, 1, (float*)dhidden, d,
-                                                                            3, nullptr);
-    GPTRIG_CHECK_LAUNCH();
-    return GPTRIG_OK;
-  }
+  const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
   gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
                                                                                       dh_acc, d, 2, nullptr);
   GPTRIG_CHECK_LAUNCH();
