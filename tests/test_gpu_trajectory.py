@@ -15,8 +15,8 @@ defined only up to the summation order.  The gate is the north star's "20-step
 loss trajectory within 1%" against that set:
   * every step's loss within 1% of one of the reference-equivalent runs (the
     closest; this GPU path's fp32 atomics add in a different order on every
-    run, and its runs fall on either side of the spike: measured over eleven
-    runs, 0.03-0.44% from the closest run, 0.08-1.18% from the 3-thread one);
+    run, and its runs fall on either side of the spike: measured over sixteen
+    runs, 0.03-0.62% from the closest run, 0.08-1.18% from the 3-thread one);
   * steps 1-5, before the chaos, within 0.1% of the fixture (all the
     equivalent runs agree there to 0.05%);
   * learning rate identical (1e-6 relative);
