@@ -56,3 +56,75 @@ def test_config_d_two_steps_match_oracle():
     worst = sorted(((abs(got_norms[k] - v) / v, k) for k, v in norms.items() if v >= 1e-2 * top), reverse=True)
     print("largest per-tensor gradient-norm differences", worst[:5], flush=True)
     assert worst[0][0] <= 5e-2, worst[:5]
+
+
+def test_config_d_bench_shape_two_micro_batches_of_64():
+    """The shape ``bench.py`` measures: 128 sequences as 2 micro-batches of 64
+    (65,536-token FLCE, B64 attention, full-size deferred weight gradients).
+    The forward is per sequence, so two sampled sequences, one from each
+    micro-batch, are checked against the oracle run on each sequence alone:
+    final hidden states (max-abs <= 3e-2 x their scale), per-token losses
+    (|d| <= 5e-3 x loss: the hidden states themselves differ by bf16
+    rounding accumulated over 12 layers, which moved single losses by up to
+    1.8e-3 relative on the box; the sequence mean to 1e-4), and eval_step's
+    masked sum over both.  One training
+    step then gives the same mean loss as the full-batch eval (same forward),
+    a finite, non-zero gradient in every tensor, and finite parameters."""
+    from gptrig.kernels import linear_cross_entropy as lce
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+    from oracle import flce as oflce
+
+    cfg = GPTConfig(layers=12, heads=12, d_model=768, vocab_size=50304, semantic_vocab_size=50304, seq_len=1024,
+                    batch_size=128, micro_batch_size=64, base_width=768, base_depth=12, embeddings="untied",
+                    optimizer=OptimizerConfig(learning_rate=2.0 ** -8, steps=20, warmup_steps=2))
+    ocfg = om.baseline_config("D", steps=20)
+    rng = np.random.default_rng(2)  # the bench's tokens
+    win = torch.from_numpy(rng.integers(0, 50304, size=(128, 1025), dtype=np.int32))
+    x, y = win[:, :-1].contiguous(), win[:, 1:].contiguous()
+    print("config D bench shape, 128 sequences as 2 x 64", flush=True)
+    trainer = GPTTrainer(cfg, seed=0)
+    params = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in om.flatten(om.init_params(ocfg, 0)).items()}
+    xg, yg = x.cuda(), y.cuda()
+    head = trainer.arena.w("output_embedding")
+    weights = torch.zeros(128, 1024)
+    want_total = 0.0
+    for seq in (5, 100):
+        micro, row = divmod(seq, 64)
+        _, _, _, xf, _, _ = trainer._forward(xg[micro * 64:(micro + 1) * 64], micro)
+        hid = xf.view(64, 1024, 768)[row]
+        tgt = yg[seq].contiguous()
+        losses, _ = lce.flce_forward(hid.contiguous(), head, tgt, 50304)
+        torch.cuda.synchronize()
+        hid_r = om.gpt_hidden(params, x[seq:seq + 1], ocfg)[0]
+        losses_r = oflce.tiled_tied_cross_entropy_losses(hid_r[None], params["output_embedding"], y[seq:seq + 1],
+                                                         semantic_vocab_size=50304, vocab_tile_size=2048,
+                                                         compute_dtype=torch.bfloat16)[0]
+        h_err = float((hid.float().cpu() - hid_r.float()).abs().max())
+        h_scale = float(hid_r.float().abs().max())
+        l_err = (losses.cpu() - losses_r).abs() / losses_r.abs()
+        print(f"sequence {seq}: hidden max-abs {h_err:.3e} (scale {h_scale:.3e}), per-token loss rel max "
+              f"{float(l_err.max()):.3e}, mean loss {float(losses.mean()):.5f} / {float(losses_r.mean()):.5f}",
+              flush=True)
+        assert h_err <= 3e-2 * h_scale, seq
+        assert float(l_err.max()) <= 5e-3, seq
+        assert abs(float(losses.mean()) - float(losses_r.mean())) <= 1e-4 * float(losses_r.mean()), seq
+        w = torch.rand(1024, generator=torch.Generator().manual_seed(seq))
+        weights[seq] = w
+        want_total += float((losses_r * w).sum())
+    total, count = trainer.eval_step(xg, yg, weights.cuda())
+    print(f"eval masked sum {float(total):.4f} / oracle {want_total:.4f}", flush=True)
+    assert abs(float(total) - want_total) <= 1e-3 * abs(want_total)
+    assert abs(float(count) - float(weights.sum())) <= 1e-5 * float(weights.sum())
+    total, count = trainer.eval_step(xg, yg, torch.ones(128, 1024, device="cuda"))
+    eval_mean = float(total) / float(count)
+    trainer.train_step(xg, yg)
+    loss, lr, gnorm = trainer.history_rows()[0]
+    print(f"step loss {loss:.5f} eval mean {eval_mean:.5f} grad norm {gnorm:.4f}", flush=True)
+    assert abs(loss - eval_mean) <= 1e-4 * eval_mean
+    assert np.isfinite(gnorm) and gnorm > 0
+    for path in trainer.arena.paths:
+        g = trainer.arena.grad(path)
+        assert bool(torch.isfinite(g).all()), path
+        assert float(g.double().norm()) > 0, path
+    assert bool(torch.isfinite(trainer.arena.p).all())

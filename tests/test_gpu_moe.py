@@ -143,3 +143,45 @@ def test_config_e_layer_shape_token_subset():
     assert maxabs(got, comb_r.reshape(64, D)) <= 3e-2 * scale(comb_r)
     got_dx = dx.reshape(B * L, D)[flat_idx.to(DEV)]
     assert maxabs(got_dx, dx_r.reshape(64, D)) <= 3e-2 * scale(dx_r)
+
+
+def test_config_e_routing_bit_exact_on_all_tokens():
+    """Config E's routing at its full size (32 x 1024 = 32,768 tokens, width
+    768, 8 experts, top-2, router ~ N(0, 0.02) as initialised): every token's
+    expert indices, the per-expert counts, the stable bucket order (one
+    1024-thread workgroup sorts all 65,536 assignments) and its inverse are
+    bit-exact against the oracle's route of the GPU's own fp32 logits, the
+    gates and probabilities within 1e-6.  A second pass plants integer logits
+    (ties) in every 16th token to exercise the lower-index rule at this size."""
+    from gptrig import _lib
+    from gptrig.moe import _route
+
+    T, D, E, k = 32 * 1024, 768, 8, 2
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.standard_normal((T, D)).astype(np.float32)).to(torch.bfloat16)
+    router_w = torch.from_numpy((rng.standard_normal((D, E)) * 0.02).astype(np.float32))
+    print(f"config E routing, {T} tokens", flush=True)
+    logits, probs, chosen, gate, counts, rows, position = _route(x.to(DEV), router_w.to(DEV), E, k)
+    torch.cuda.synchronize()
+    probs_r, chosen_r, gate_r, order_r, _, counts_r, rows_r = omoe.route(logits.cpu(), E, k)
+    assert torch.equal(chosen.cpu(), chosen_r)
+    assert torch.equal(counts.cpu(), counts_r)
+    assert torch.equal(rows.cpu().long(), rows_r)
+    inv = torch.empty_like(order_r)
+    inv[order_r] = torch.arange(T * k)
+    assert torch.equal(position.cpu().long(), inv)
+    assert maxabs(gate, gate_r) <= 1e-6 and maxabs(probs, probs_r) <= 1e-6
+
+    tied = logits.cpu().clone()
+    tied[::16] = torch.from_numpy(rng.integers(-2, 3, size=(T // 16, E)).astype(np.float32))
+    probs_r, chosen_r, gate_r, order_r, _, counts_r, rows_r = omoe.route(tied, E, k)
+    lg = tied.to(DEV)
+    order = torch.empty(T * k, dtype=torch.int32, device=DEV)
+    _lib.call("gptrig_moe_route", lg.data_ptr(), probs.data_ptr(), chosen.data_ptr(), gate.data_ptr(),
+              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), None, 0, T, E, k,
+              _lib.stream())
+    torch.cuda.synchronize()
+    assert torch.equal(chosen.cpu(), chosen_r)
+    assert torch.equal(counts.cpu(), counts_r)
+    assert torch.equal(order.cpu().long(), order_r)
+    assert torch.equal(rows.cpu().long(), rows_r)

@@ -111,6 +111,67 @@ def test_train_step_completep_clip_and_residual_scale_match_oracle():
         assert abs(ratio - 1) <= 0.1 and cos >= 0.9, path
 
 
+def test_train_step_batch_data_ratio_matches_oracle():
+    """The fixed-TPP transfer rule away from ratio 1: batch_multiplier 2 over
+    data_multiplier 0.5 (train.py:792-800) gives betas 0.6 / 0.8
+    (:1336-1345), the learning rate x 2 (:1231), epsilon x 1/2 and weight
+    decay x 2 (:1413-1414).  Weight decay 20 and epsilon 1e-3 make the decay
+    and epsilon terms a visible part of every update: on the CPU, the oracle
+    with the decay horizon inverted moves the weight updates' norms by a
+    factor 0.44-0.57, with the epsilon horizon inverted the norm-scale
+    update by 0.48, and with the LR horizon inverted every update by 0.25;
+    a slip in the betas (1 - (1 - beta) / ratio) shows in the Adam moments,
+    compared tensor by tensor as well."""
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+
+    steps = 4
+    common = dict(layers=2, heads=2, d_model=128, vocab_size=1000, semantic_vocab_size=997, seq_len=128,
+                  batch_size=4, base_width=128, base_depth=2, attention_scale="inverse_sqrt_head_dim",
+                  embeddings="untied")
+    opt = dict(learning_rate=2.0 ** -9, steps=steps, warmup_steps=1, weight_decay=20.0, adam_epsilon=1.0e-3,
+               batch_multiplier=2.0, data_multiplier=0.5)
+    ocfg = om.Config(**common, attention_backend="flash", optimizer=oopt.OptimizerConfig(**opt))
+    gcfg = GPTConfig(**common, micro_batch_size=2, optimizer=OptimizerConfig(**opt))
+    print("train case batch_multiplier 2, data_multiplier 0.5", flush=True)
+    assert oopt.effective_adam_betas(ocfg.optimizer) == pytest.approx((0.6, 0.8), abs=1e-12)
+    windows = om.synthetic_windows(6, steps, 4, 128, 997)
+    state = om.init_state(ocfg, 0)
+    trainer = GPTTrainer(gcfg, seed=0)
+    assert (trainer.beta1, trainer.beta2) == pytest.approx((0.6, 0.8), abs=1e-12)
+    for i in range(steps):
+        w = torch.from_numpy(windows[i])
+        om.train_step(state, w[:, :-1], w[:, 1:], ocfg)
+        trainer.train_step(w[:, :-1].cuda(), w[:, 1:].cuda())
+    got = trainer.history_rows()
+    want = np.asarray(state.history)
+    print("gpu   ", got.tolist(), flush=True)
+    print("oracle", want.tolist(), flush=True)
+    # Step 2 (one step into the cosine over 3): base 2^-9 x 2 x (0.1 + 0.9 x 0.75).
+    assert abs(want[1, 1] - 2.0 ** -9 * 2 * (0.1 + 0.9 * 0.75)) < 1e-9
+    assert abs(got[0, 0] - want[0, 0]) <= 1e-3 * want[0, 0]
+    assert np.all(np.abs(got[:, 0] - want[:, 0]) <= 1e-2 * want[:, 0])
+    np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-6)
+    assert np.all(np.abs(got[:, 2] - want[:, 2]) <= 2e-2 * want[:, 2])
+    init = om.flatten(om.init_params(ocfg, 0))
+    for path in ("blocks/0/qkv_w", "blocks/1/mlp_up_w", "blocks/1/mlp_down_b", "blocks/0/ln2_scale",
+                 "token_embedding", "output_embedding"):
+        p0 = torch.from_numpy(np.asarray(init[path]))
+        du = (trainer.arena.param(path).cpu() - p0).double().reshape(-1)
+        dw = (state.params[path] - p0).double().reshape(-1)
+        ratio = float(du.norm() / dw.norm())
+        cos = float(du @ dw / (du.norm() * dw.norm()))
+        print(f"{path}: update norm ratio {ratio:.4f}, cosine {cos:.4f}", flush=True)
+        assert abs(ratio - 1) <= 0.1 and cos >= 0.9, path
+        for name, arena, ref in (("m", trainer.arena.m, state.m), ("v", trainer.arena.v, state.v)):
+            got_mom = trainer.arena._view(arena, path).cpu().double().reshape(-1)
+            want_mom = ref[path].double().reshape(-1)
+            r = float(got_mom.norm() / want_mom.norm())
+            c = float(got_mom @ want_mom / (got_mom.norm() * want_mom.norm()))
+            print(f"  {name}: norm ratio {r:.4f}, cosine {c:.4f}", flush=True)
+            assert abs(r - 1) <= 0.1 and c >= 0.9, (path, name)
+
+
 def test_initial_parameters_are_bit_identical_to_the_reference_draws():
     from gptrig.train import GPTTrainer
 

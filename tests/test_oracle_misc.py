@@ -125,6 +125,120 @@ def test_adamw_first_two_steps_by_hand():
     assert abs(float(p["blocks/0/qkv_w"][0]) - (float(w1[0]) - lr2 * (mh / (math.sqrt(vh) + 1e-8) + 0.1 * float(w1[0])))) < 1e-6
 
 
+def ratio_four(module, **kw):
+    """batch_multiplier / data_multiplier = 2 / 0.5 = 4 (train.py:792-800: batch / anchor and
+    tpp / base tpp); epsilon 0.2 so that its horizon factor shows in the update."""
+    base = dict(learning_rate=0.01, warmup_steps=0, steps=1000, weight_decay=0.1, adam_epsilon=0.2,
+                batch_multiplier=2.0, data_multiplier=0.5)
+    base.update(kw)
+    return module.OptimizerConfig(**base)
+
+
+def test_batch_data_ratio_four_betas_and_learning_rate_by_hand():
+    """train.py:1336-1345 and :1231 at ratio 4: beta1 = 1 - 0.1 * 4 = 0.6,
+    beta2 = 1 - 0.05 * 4 = 0.8, and the learning rate doubles (sqrt 4).  The
+    plausible slips give other numbers: betas 1 - (1 - beta) / 4 = 0.975 /
+    0.9875, or the horizon sqrt(data / batch) = 1/2 (a factor 4 off)."""
+    cfg = ratio_four(oopt)
+    b1, b2 = oopt.effective_adam_betas(cfg)
+    assert abs(b1 - 0.6) < 1e-12 and abs(b2 - 0.8) < 1e-12
+    # Constant learning rate after a 10-step warmup over 10 + 1000 steps at step 10: base x 2.
+    flat = ratio_four(oopt, warmup_steps=10, steps=1010, min_lr_ratio=1.0)
+    assert abs(oopt.learning_rate(10, flat) - 0.02) < 1e-9
+    assert abs(oopt.learning_rate(5, flat) - 0.01) < 1e-9  # half-way through the warmup
+    # The same ratio from other multipliers gives the same numbers (only batch / data enters).
+    other = ratio_four(oopt, batch_multiplier=4.0, data_multiplier=1.0, warmup_steps=10, steps=1010, min_lr_ratio=1.0)
+    assert oopt.effective_adam_betas(other) == pytest.approx((0.6, 0.8), abs=1e-12)
+    assert abs(oopt.learning_rate(10, other) - 0.02) < 1e-9
+
+
+def test_batch_data_ratio_four_adamw_two_steps_by_hand():
+    """Two AdamW updates at ratio 4 (train.py:1386-1445) worked by hand:
+    epsilon 0.2 x sqrt(1/4) = 0.1, weight decay 0.1 x sqrt(4) = 0.2, betas
+    0.6 / 0.8, learning rate 0.01 x 2 x cosine(step)."""
+    cfg = ratio_four(oopt)
+    p = {"blocks/0/qkv_w": torch.tensor([1.0, -2.0]), "blocks/0/qkv_b": torch.tensor([0.5])}
+    m = {k: torch.zeros_like(v) for k, v in p.items()}
+    v = {k: torch.zeros_like(v) for k, v in p.items()}
+    g1 = {"blocks/0/qkv_w": torch.tensor([0.3, -0.1]), "blocks/0/qkv_b": torch.tensor([2.0])}
+    lr1, _ = oopt.adamw_step(p, g1, m, v, 1, cfg)
+    assert abs(lr1 - 0.02 * (0.1 + 0.45 * (1 + math.cos(math.pi / 1000)))) < 1e-8
+    # Step 1: m = 0.4 g, v = 0.2 g^2; bias corrections 0.4 and 0.2 give m^ = g, v^ = g^2,
+    # so adam = g / (|g| + 0.1): 0.3 / 0.4 = 0.75, -0.1 / 0.2 = -0.5, 2 / 2.1.
+    np.testing.assert_allclose(p["blocks/0/qkv_w"].numpy(),
+                               [1.0 - lr1 * (0.75 + 0.2 * 1.0), -2.0 - lr1 * (-0.5 + 0.2 * -2.0)], rtol=1e-6)
+    np.testing.assert_allclose(p["blocks/0/qkv_b"].numpy(), [0.5 - lr1 * (2.0 / 2.1)], rtol=1e-6)
+    np.testing.assert_allclose(m["blocks/0/qkv_w"].numpy(), [0.12, -0.04], rtol=1e-6)
+    np.testing.assert_allclose(v["blocks/0/qkv_w"].numpy(), [0.018, 0.002], rtol=1e-6)
+    # Step 2 with g2 = (-0.1, 0.2): m = 0.6 * (0.12, -0.04) + 0.4 * (-0.1, 0.2) = (0.032, 0.056),
+    # v = 0.8 * (0.018, 0.002) + 0.2 * (0.01, 0.04) = (0.0164, 0.0096); corrections 1 - 0.36 = 0.64
+    # and 1 - 0.64 = 0.36.
+    w1 = p["blocks/0/qkv_w"].clone().double()
+    g2 = {"blocks/0/qkv_w": torch.tensor([-0.1, 0.2]), "blocks/0/qkv_b": torch.tensor([-1.0])}
+    lr2, _ = oopt.adamw_step(p, g2, m, v, 2, cfg)
+    np.testing.assert_allclose(m["blocks/0/qkv_w"].numpy(), [0.032, 0.056], rtol=1e-6)
+    np.testing.assert_allclose(v["blocks/0/qkv_w"].numpy(), [0.0164, 0.0096], rtol=1e-6)
+    adam = [(0.032 / 0.64) / (math.sqrt(0.0164 / 0.36) + 0.1), (0.056 / 0.64) / (math.sqrt(0.0096 / 0.36) + 0.1)]
+    want = [float(w1[i]) - lr2 * (adam[i] + 0.2 * float(w1[i])) for i in range(2)]
+    np.testing.assert_allclose(p["blocks/0/qkv_w"].double().numpy(), want, rtol=1e-6)
+    # A slip in any horizon factor moves these updates by far more than the tolerance.
+    assert abs(adam[0] - (0.032 / 0.64) / (math.sqrt(0.0164 / 0.36) + 0.4)) > 0.05
+
+
+def test_batch_data_ratio_rejects_invalid_momenta():
+    """train.py:1340-1344: beta1 = 1 - 0.1 * ratio leaves [0, 1) above ratio 10,
+    and ratio 0 gives beta = 1."""
+    for module in (oopt,):
+        assert module.effective_adam_betas(ratio_four(module, batch_multiplier=10.0, data_multiplier=1.0))[0] < 1e-12
+        with pytest.raises(ValueError):
+            module.effective_adam_betas(ratio_four(module, batch_multiplier=10.5, data_multiplier=1.0))
+        with pytest.raises(ValueError):
+            module.effective_adam_betas(ratio_four(module, batch_multiplier=0.0, data_multiplier=1.0))
+
+
+def test_router_statistics_closed_forms():
+    """routed_mlp_local's summary (reference_moe/train.py:1290-1306): the
+    mean over tokens of the softmax entropy (with its +1e-9), the mean top-1
+    gate, and the root of the mean squared logit.
+      * Rows of equal logits c_r: entropy -log(1/E + 1e-9), top-1 gate 1/k,
+        RMS sqrt(mean c_r^2) (c = 1 and 3: sqrt 5, where a mean |logit| would
+        give 2).
+      * Rows (ln 7, 0, ..., 0) with E = 8: probabilities 1/2 and 1/14, entropy
+        (1/2) ln 2 + (1/2) ln 14, top-2 gate (7/8, 1/8).
+      * Half of each: the entropy is the mean of the two (the entropy of the
+        mean probability would be larger)."""
+    E, k = 8, 2
+
+    def summary(logits: torch.Tensor) -> torch.Tensor:
+        # The router sees the given logits: identity token rows times router_w = logits.
+        t = logits.shape[0]
+        xs = torch.eye(t).reshape(1, t, t)
+        out = omoe.routed_mlp_local(xs, logits, torch.zeros(E, t, 3), torch.zeros(E, 3), torch.zeros(E, 3, t),
+                                    torch.zeros(E, t), experts=E, top_k_count=k, dtype=torch.float32)
+        return out[3].double()
+
+    uniform = torch.tensor([[1.0] * E, [3.0] * E])
+    s = summary(uniform)
+    assert abs(float(s[0]) + math.log(1 / E + 1e-9)) < 1e-6
+    assert abs(float(s[1]) - 0.5) < 1e-7
+    assert abs(float(s[2]) - math.sqrt(5.0)) < 1e-6
+    peaked = torch.tensor([[math.log(7.0)] + [0.0] * (E - 1)] * 2)
+    s = summary(peaked)
+    h_peak = -(0.5 * math.log(0.5 + 1e-9) + 7 * (1 / 14) * math.log(1 / 14 + 1e-9))
+    assert abs(h_peak - (0.5 * math.log(2) + 0.5 * math.log(14))) < 1e-7
+    assert abs(float(s[0]) - h_peak) < 1e-6
+    assert abs(float(s[1]) - 7 / 8) < 1e-6
+    assert abs(float(s[2]) - math.log(7.0) / math.sqrt(E)) < 1e-6
+    mixed = torch.cat([uniform[:1], peaked[:1]])
+    s = summary(mixed)
+    h_uniform = -math.log(1 / E + 1e-9)
+    assert abs(float(s[0]) - (h_uniform + h_peak) / 2) < 1e-6
+    pbar = torch.tensor([1 / E] * E) / 2 + torch.tensor([0.5] + [1 / 14] * (E - 1)) / 2
+    assert float(-(pbar * torch.log(pbar)).sum()) - float(s[0]) > 0.05
+    assert abs(float(s[1]) - (0.5 + 7 / 8) / 2) < 1e-6
+    assert abs(float(s[2]) - math.sqrt((E * 1.0 + math.log(7.0) ** 2) / (2 * E))) < 1e-6
+
+
 def test_weight_decay_mask_roles():
     assert oopt.decays("token_embedding") and oopt.decays("blocks/0/mlp_up_w")
     assert not oopt.decays("blocks/0/mlp_up_b") and not oopt.decays("final_ln_scale")

@@ -56,9 +56,14 @@ def test_noalloc_forward_equals_the_workspace_entry_point():
 def test_noalloc_forward_rejects_sizes_past_its_scratch():
     from gptrig import _lib
 
-    h, w, t = inputs(8, 64, 256, 256, 73)
     n = 24000  # 24000 tokens x 197 tiles x 8 B + 4 B per token > 32 MiB
+    # Buffers of the full size, so that a host check that stopped rejecting
+    # this call would show as a wrong return code, not as accesses past them.
+    h, w, t = inputs(n, 768, 50304, 50304, 73)
+    losses = torch.empty(n, dtype=torch.float32, device="cuda")
+    lse = torch.empty(n, dtype=torch.float32, device="cuda")
     assert _lib.query("gptrig_flce_fwd_workspace_bytes", n, 768, 50304) > 32 << 20
-    rc = _lib.lib().gptrig_flce_fwd_noalloc(h.data_ptr(), w.data_ptr(), t.data_ptr(), h.data_ptr(), h.data_ptr(),
-                                            n, 768, 50304, 50304, _lib.stream())
+    rc = _lib.lib().gptrig_flce_fwd_noalloc(h.data_ptr(), w.data_ptr(), t.data_ptr(), losses.data_ptr(),
+                                            lse.data_ptr(), n, 768, 50304, 50304, _lib.stream())
+    torch.cuda.synchronize()
     assert rc == E_WORKSPACE
