@@ -35,12 +35,12 @@ import torch  # noqa: E402
 METRIC = "train tokens/s at 125M S=1024; attn-bwd + FLCE TFLOP/s as % of bf16 MFMA peak"
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # HBM bytes of one FLCE fwd+bwd launch sequence (the trainer's kept-softmax
-# pair), by micro-batch tokens N (d 768, V 50304): FETCH_SIZE (x 2.0, the factor the counter
+# pairs), by (micro-batch tokens N, tokens per chunk) (d 768, V 50304): FETCH_SIZE (x 2.0, the factor the counter
 # reads for a 256 MiB copy) + WRITE_SIZE (x 1.0) summed over its launches, from
 # `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes; a shape without a measurement reports null.
-FLCE_TRAFFIC_BYTES = {65536: (31112 + 13942) * 2 ** 20}
+FLCE_TRAFFIC_BYTES = {(65536, 65536): (31112 + 13942) * 2 ** 20}
 
 
 def parse_args():
@@ -76,11 +76,23 @@ def traffic_pass(micro_batch: int) -> None:
     h = torch.randn(n, d, device=dev).bfloat16()
     w = (torch.randn(vocab, d, device=dev) * 0.02).bfloat16()
     t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32)
-    # The trainer's FLCE sequence: the kept-softmax forward and backward.
-    _, lse, keep = lce.flce_forward_keep(h, w, t, vocab)
-    lce.flce_backward_keep(h, w, t, lse, keep, None, 1.0 / n, vocab)
-    del keep
-    torch.cuda.synchronize()
+    # The trainer's FLCE sequence: kept-softmax forward and backward per token
+    # chunk (bounded by the default vocab_tile_size), then the same over one
+    # chunk of all tokens (flce_whole_vocab).
+    from gptrig.train import flce_token_chunk
+
+    dw = torch.empty(vocab, d, device=dev)
+    for chunk in (flce_token_chunk(n, vocab, 2048, False), n):
+        keep = None
+        for c0 in range(0, n, chunk):
+            c1 = min(n, c0 + chunk)
+            _, lse, keep = lce.flce_forward_keep(h[c0:c1], w, t[c0:c1], vocab, keep)
+            lce.flce_backward_keep(h[c0:c1], w, t[c0:c1], lse, keep, None, 1.0 / n, vocab, dweight=dw,
+                                   accumulate=c0 > 0)
+        torch.cuda.synchronize()
+        del keep
+        print(f"flce sequence with token chunks of {chunk} done", flush=True)
+    del dw
     q, k, v, do = (torch.randn(micro_batch, 12, 1024, 64, device=dev).bfloat16() for _ in range(4))
     o, lse2 = fa.flash_forward(q, k, v, None, 0.125)
     fa.flash_backward(q, k, v, o, lse2, do, None, 0.125)
@@ -152,20 +164,34 @@ def isolated_configs(reps: int = 20) -> dict:
             lce.flce_backward(h, w, t, lse_c, None, 1.0 / n, vocab, chunk)
         return run
 
+    from gptrig.train import flce_token_chunk
+
     keep_buf = []
+    dw = torch.empty(vocab, d, device=dev)
 
-    def flce_keep():
-        _, lse_c, kb = lce.flce_forward_keep(h, w, t, vocab, keep_buf[0] if keep_buf else None)
-        if not keep_buf:
-            keep_buf.append(kb)
-        lce.flce_backward_keep(h, w, t, lse_c, kb, None, 1.0 / n, vocab)
+    def flce_keep(chunk):
+        def run():
+            for c0 in range(0, n, chunk):
+                c1 = min(n, c0 + chunk)
+                _, lse_c, kb = lce.flce_forward_keep(h[c0:c1], w, t[c0:c1], vocab, keep_buf[0] if keep_buf else None)
+                keep_buf[:] = [kb]
+                lce.flce_backward_keep(h[c0:c1], w, t[c0:c1], lse_c, kb, None, 1.0 / n, vocab, dweight=dw,
+                                       accumulate=c0 > 0)
+        return run
 
-    # The trainer's path (whole vocabulary, kept softmax), the same chunk with
-    # the logits recomputed, and the public API's default vocab_tile_size
-    # (2048: the reference's bounded [tokens, tile] working set).
-    flce_ms = timed(flce_keep)
+    # The trainer's path (kept softmax over token chunks bounded by the default
+    # vocab_tile_size), the same over one chunk of all tokens, the whole
+    # vocabulary with the logits recomputed, and the public API's default
+    # vocab_tile_size (2048: the reference's bounded [tokens, tile] working set).
+    chunk = flce_token_chunk(n, vocab, lce.DEFAULT_VOCAB_TILE_SIZE, False)
+    flce_ms = timed(flce_keep(chunk))
     flce_tf = flce_flops(n, d, vocab) / (flce_ms / 1e3) / 1e12
+    keep_bytes = keep_buf[0].numel()
     keep_buf.clear()
+    one_ms = timed(flce_keep(n))
+    one_tf = flce_flops(n, d, vocab) / (one_ms / 1e3) / 1e12
+    keep_buf.clear()
+    del dw
     whole_ms = timed(flce_with(lce.grad_chunk(n, vocab)))
     whole_tf = flce_flops(n, d, vocab) / (whole_ms / 1e3) / 1e12
     tile_ms = timed(flce_with(lce.chunk_for(lce.DEFAULT_VOCAB_TILE_SIZE)))
@@ -178,7 +204,10 @@ def isolated_configs(reps: int = 20) -> dict:
             "bwd_algorithmic_flops": attn_bwd_flops(B, H, S, D)},
         "flce_N16384_d768_V50304": {"ms": round(flce_ms, 4), "tflops": round(flce_tf, 1),
                                     "frac": round(flce_tf / peak, 4), "algorithmic_flops": flce_flops(n, d, vocab),
-                                    "path": "whole vocabulary, kept softmax (the trainer's opt-in)",
+                                    "path": f"kept softmax over token chunks of {chunk} (the trainer's default: "
+                                            f"{keep_bytes} kept bytes <= tokens x 2048 x 4)",
+                                    "one_chunk_kept": {"ms": round(one_ms, 4), "tflops": round(one_tf, 1),
+                                                       "frac": round(one_tf / peak, 4)},
                                     "whole_vocabulary_recompute": {"ms": round(whole_ms, 4),
                                                                    "tflops": round(whole_tf, 1),
                                                                    "frac": round(whole_tf / peak, 4)},
@@ -186,6 +215,47 @@ def isolated_configs(reps: int = 20) -> dict:
                                                           "frac": round(tile_tf / peak, 4),
                                                           "workspace_bytes": lce.workspace_bytes(n, d, vocab)}},
     }
+
+
+def flce_whole_vocab(n: int, d: int, vocab: int, reps: int = 5) -> dict:
+    """The FLCE of one micro-batch (n tokens) as one chunk over all tokens
+    (``GPTConfig.flce_whole_vocab``: fp16 [vocab, n] kept probabilities, not
+    bounded by vocab_tile_size), timed with HIP events on its stream over
+    ``reps`` launch sequences after one untimed."""
+
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(n, d, device=dev, generator=g).bfloat16()
+    w = (torch.randn(vocab, d, device=dev, generator=g) * 0.02).bfloat16()
+    t = torch.randint(0, vocab, (n,), device=dev, dtype=torch.int32, generator=g)
+    dw = torch.empty(vocab, d, device=dev)
+    keep = []
+
+    def run():
+        _, lse, kb = lce.flce_forward_keep(h, w, t, vocab, keep[0] if keep else None)
+        keep[:] = [kb]
+        lce.flce_backward_keep(h, w, t, lse, kb, None, 1.0 / n, vocab, dweight=dw)
+
+    run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    tf = flce_flops(n, d, vocab) / (ms / 1e3) / 1e12
+    traffic = FLCE_TRAFFIC_BYTES.get((n, n))
+    out = {"kernel": f"flce fwd+bwd, one kept-softmax chunk over all {n} tokens ([vocab, tokens] fp16, "
+                     "GPTConfig.flce_whole_vocab)", "bound": "mfma", "achieved": round(tf, 1),
+           "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+           "traffic": traffic, "ms": round(ms, 3), "kept_bytes": int(keep[0].numel())}
+    del h, w, t, dw, keep
+    torch.cuda.empty_cache()
+    return out
 
 
 def attn_bwd_flops(batch, heads, seq, head_dim):
@@ -290,17 +360,16 @@ def cpu_baseline() -> dict:
     except (OSError, StopIteration):
         pass
     return {
-        "value": round(128 * 1024 / d_step, 1),
+        "value": round(cfg_a.batch_size * cfg_a.seq_len / a_step, 1),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "extrapolated": True,
         "sample": (f"CPU restatement of reference semantics (oracle/, torch-CPU fp32 math with bf16 rounding), "
-                   f"{threads} threads on {cpu}.  value: config D (125M) tokens/s EXTRAPOLATED from a measured "
-                   f"per-sequence forward+backward ({t_fb:.2f} s, median of 3 after a warm-up) x 128 sequences "
-                   f"+ one AdamW update ({t_adam:.2f} s)"),
-        "config_A_step": {"tokens_per_s": round(cfg_a.batch_size * cfg_a.seq_len / a_step, 1),
-                          "s_per_step": round(a_step, 3), "measured": "median of 5 full steps after 2 warm-ups"},
+                   f"{threads} threads on {cpu}.  value: config A (8L d512, the reference's CPU-runnable step: "
+                   f"8 x 1024 tokens) full train step, median of 5 steps after 2 warm-ups ({a_step:.2f} s/step)"),
+        "config_D_extrapolated": {"tokens_per_s": round(128 * 1024 / d_step, 1), "extrapolated": True,
+                                  "from": f"a measured per-sequence forward+backward ({t_fb:.2f} s, median of 3 "
+                                          f"after a warm-up) x 128 sequences + one AdamW update ({t_adam:.2f} s)"},
         "config_B_attention_fwd_bwd_s": round(b_s, 3),
         "config_C_flce_fwd_bwd_s": round(c_s, 3),
     }
@@ -358,7 +427,7 @@ def main():
         sys.exit(2)
 
     from gptrig.optim import OptimizerConfig
-    from gptrig.train import GPTConfig, GPTTrainer
+    from gptrig.train import GPTConfig, GPTTrainer, flce_token_chunk
 
     cfg = GPTConfig(layers=12, heads=12, d_model=768, mlp_mult=4, vocab_size=50304, semantic_vocab_size=50304,
                     seq_len=1024, batch_size=128, micro_batch_size=args.micro_batch,
@@ -396,10 +465,11 @@ def main():
 
     n_micro = cfg.batch_size // cfg.micro_batch_size
     mb_tokens = cfg.micro_batch_size * cfg.seq_len
-    traffic = FLCE_TRAFFIC_BYTES.get(mb_tokens)  # measured per shape; None for an unmeasured one
-    # FLCE: one forward + one backward launch per micro-batch; report per micro-batch (fwd+bwd).
+    chunk = flce_token_chunk(mb_tokens, cfg.vocab_size, cfg.vocab_tile_size, cfg.flce_whole_vocab)
+    traffic = FLCE_TRAFFIC_BYTES.get((mb_tokens, chunk))  # measured per shape; None for an unmeasured one
+    # FLCE: every timed launch sequence of the step, per micro-batch (fwd + bwd of all its token chunks).
     flce_ms_launch, flce_n = avg_ms("flce")
-    flce_ms = 2 * flce_ms_launch
+    flce_ms = flce_ms_launch * flce_n / (n_micro * args.steps)
     flce_tf = flce_flops(mb_tokens, cfg.d_model, cfg.vocab_size) / (flce_ms / 1e3) / 1e12
     ab_ms, _ = avg_ms("attn_bwd")
     ab_tf = attn_bwd_flops(cfg.micro_batch_size, cfg.heads, cfg.seq_len, cfg.head_dim) / (ab_ms / 1e3) / 1e12
@@ -427,8 +497,9 @@ def main():
                                f"{cfg.micro_batch_size}, AdamW",
                    "global_batch": cfg.batch_size, "micro_batch": cfg.micro_batch_size, "seq_len": cfg.seq_len,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": f"flce (fused LM-head cross-entropy fwd+bwd, kept softmax, per "
-                               f"{cfg.micro_batch_size}x1024-token micro-batch)",
+        "roofline": {"kernel": f"flce (fused LM-head cross-entropy fwd+bwd per {cfg.micro_batch_size}x1024-token "
+                               f"micro-batch: kept softmax over token chunks of {chunk}, bounded by vocab_tile_size "
+                               f"{cfg.vocab_tile_size} like the reference's tiled loss)",
                      "bound": "mfma", "achieved": round(flce_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flce_tf / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": traffic, "traffic_GBps": None if traffic is None else round(traffic / flce_ms / 1e6, 1),
@@ -445,6 +516,7 @@ def main():
     }
     del trainer
     torch.cuda.empty_cache()
+    result["roofline_flce_whole_vocab"] = flce_whole_vocab(mb_tokens, cfg.d_model, cfg.vocab_size)
     if not args.no_extra and args.micro_batch != 32:
         # BASELINE.json's split of the same step: 4 micro-batches of 32.
         split = GPTTrainer(replace(cfg, micro_batch_size=32), seed=0, history_steps=7)

@@ -460,17 +460,30 @@ __global__ void __launch_bounds__(gemm::THREADS)
     const int n = tn * BN + 64 * wn + 32 * nb + l32;
     if (n >= N) continue;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m0 = tm * BM + 128 * wm + 32 * mb + 4 * hl;
+      float* const dst = C + (int64_t)m0 * ldc + n;
+      auto row = [&](int i) { return 8 * (i >> 2) + (i & 3); };
+      if (mode == 1) {
+        // Read-modify-write: the block's 16 reads are issued together, so
+        // their latencies overlap instead of each add waiting for its read.
+        float old[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = tm * BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (m >= M) continue;
-        float* dst = C + (int64_t)m * ldc + n;
-        if (mode == 2)
-          atomicAdd(dst, acc[mb][nb][i]);
-        else
-          *dst = mode ? *dst + acc[mb][nb][i] : acc[mb][nb][i];
+        for (int i = 0; i < 16; ++i) old[i] = m0 + row(i) < M ? dst[(int64_t)row(i) * ldc] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (m0 + row(i) < M) dst[(int64_t)row(i) * ldc] = old[i] + acc[mb][nb][i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (m0 + row(i) >= M) continue;
+          if (mode == 2)
+            atomicAdd(dst + (int64_t)row(i) * ldc, acc[mb][nb][i]);
+          else
+            dst[(int64_t)row(i) * ldc] = acc[mb][nb][i];
+        }
       }
+    }
   }
 }
 
@@ -903,6 +916,28 @@ int gptrig_flce_fwd_keep(const void* hidden, const void* weight, const int32_t* 
 
 namespace {
 
+// Token split of the kept-softmax dW GEMM (tiles 256x256 output tiles over
+// k_iters 32-token stages), from an estimate in units of one stage: each round
+// of CU-sized waves costs its stages plus its epilogue, about 60 stages for a
+// split's fp32 atomic add of a 256 KB tile into the large dW array, 20 for a
+// read-modify-write and 10 for a plain store (measured at 5120 and 65536
+// tokens per call).
+int dweight_split(unsigned tiles, int k_iters, bool accumulate) {
+  const int cus = gemm::device_cus();
+  int best = 1;
+  double best_cost = 1e300;
+  for (int sp = 1; sp <= 16 && (sp == 1 || k_iters / sp >= 8); ++sp) {
+    const double rounds = (double)ceil_div((int64_t)tiles * sp, (int64_t)cus);
+    const double epi = sp > 1 ? 60.0 : (accumulate ? 20.0 : 10.0);
+    const double cost = rounds * ((double)ceil_div(k_iters, sp) + epi);
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = sp;
+    }
+  }
+  return best;
+}
+
 int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targets, float* losses, float* lse,
                     void* workspace, int n, int d, int vocab, int semantic_vocab, hipStream_t s, void* keep) {
   const int ntiles = ceil_div(vocab, BM);
@@ -1089,7 +1124,14 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
   float* dh_acc = (float*)workspace;
   const bf16* Wp = (const bf16*)weight;
   const bf16* Hp = (const bf16*)hidden;
-  if (!accumulate_dweight) {
+  // dW = G^T h over this call's n tokens: split over the tokens (fp32 atomics)
+  // only when that beats one workgroup per output tile (plain store, or
+  // read-modify-write when accumulating).  With few tokens per call (a token
+  // chunk of a bounded run) the split's atomic epilogues dominate.
+  const int vc = vocab;
+  const int dw_split = dweight_split(tiles_of(vc, d), ceil_div(n, gemm::BK), accumulate_dweight != 0);
+  const int dw_mode = dw_split > 1 ? 2 : (accumulate_dweight ? 1 : 0);
+  if (!accumulate_dweight && dw_split > 1) {
     const int64_t total = (int64_t)vocab * d;
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
     GPTRIG_CHECK_LAUNCH();
@@ -1107,12 +1149,10 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
   flce_keep_rescale_kernel<<<rgrid, 256, 0, s>>>(gt, alpha, n, vocab, semantic_vocab, targets, cotangent,
                                                   cotangent_scale);
   GPTRIG_CHECK_LAUNCH();
-  // dW += G^T h and dh += G W, as in gptrig_flce_bwd's one-chunk path.
-  const int vc = vocab;
+  // dW (+)= G^T h and dh += G W.
   Operand Ag{gt, n, vc}, Bh{Hp, d};
-  const int dw_split = gemm::choose_split(tiles_of(vc, d), ceil_div(n, gemm::BK));
   gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(Ag, Bh, vc, d, n, dw_split,
-                                                                                      dweight, d, 2, nullptr);
+                                                                                      dweight, d, dw_mode, nullptr);
   GPTRIG_CHECK_LAUNCH();
   Operand Agt{gt, n, vc}, Bw{Wp, d};
   const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));

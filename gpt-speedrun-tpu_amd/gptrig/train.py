@@ -73,12 +73,15 @@ class GPTConfig:
     expert_top_k: int = 2
     expert_mult: int = 2
     router_aux_coefficient: float = 0.01
-    # The backward's FLCE vocabulary chunk: True = one chunk over the whole
-    # vocabulary while its bf16 [tokens, vocab] gradient fits 8 GiB (the
-    # fastest choice on one MI355X), with the forward keeping its
-    # probabilities in that array so the backward skips the logits recompute;
-    # False = vocab_tile_size, the reference's bounded [tokens, tile] working set.
-    flce_whole_vocab: bool = True
+    # FLCE working set.  False (the default): bounded like the reference's
+    # tiled loss (linear_cross_entropy.py:1-24, at most [tokens, vocab_tile_size]
+    # fp32 logits live): the micro-batch's tokens are cut into chunks whose
+    # kept fp16 probabilities [vocab, chunk] take at most tokens x
+    # vocab_tile_size x 4 bytes, and each chunk's forward and backward run
+    # back to back (the loss is the step's last node, so its cotangent is
+    # known).  True: one chunk over all tokens ([vocab, tokens] fp16, 6.6 GB
+    # at 65536 tokens; fastest on one MI355X).
+    flce_whole_vocab: bool = False
     optimizer: OptimizerConfig = field(default_factory=OptimizerConfig)
 
     @property
@@ -162,6 +165,28 @@ def init_params(config: GPTConfig, seed: int) -> dict[str, np.ndarray]:
     if config.embeddings == "untied":
         flat["output_embedding"] = normal(rng, (config.vocab_size, d), config.init_std / config.width_multiplier)
     return flat
+
+
+def flce_token_chunk(tokens: int, vocab: int, vocab_tile_size: int, whole: bool) -> int:
+    """Tokens per kept-softmax FLCE chunk of a micro-batch.
+
+    ``whole``: all of them.  Otherwise the largest multiple of 64 tokens whose
+    kept buffer (``gptrig_flce_keep_bytes``: fp16 probabilities over the
+    padded vocabulary plus the per-row maxima) fits ``tokens x
+    vocab_tile_size x 4`` bytes, the reference's fp32 ``[tokens,
+    vocab_tile_size]`` live logits (``linear_cross_entropy.py:1-24``), at
+    least 64; then evened out over the chunks it needs.
+    """
+
+    if whole:
+        return tokens
+    per64 = _lib.query("gptrig_flce_keep_bytes", 64, vocab)
+    budget = tokens * vocab_tile_size * 4
+    cap = max(1, budget // per64) * 64
+    if cap >= tokens:
+        return tokens
+    share = -(-tokens // -(-tokens // cap))  # an even share of the chunks needed, <= cap
+    return -(-share // 64) * 64  # still <= cap, a multiple of 64
 
 
 class ParamArena:
@@ -481,20 +506,32 @@ class GPTTrainer:
         head = A.w(self.head_path)
         losses = torch.empty(N, dtype=F32, device=self.device)
         lse_ce = torch.empty(N, dtype=F32, device=self.device)
-        ws = self._workspace("flce_fwd", _lib.query("gptrig_flce_fwd_workspace_bytes", N, d, c.vocab_size))
-        # With the whole-vocabulary opt-in the forward keeps its probabilities
-        # (fp16 [vocab, N]) and the backward rescales them instead of
-        # recomputing the logits GEMM.
-        keep = None
-        if (c.flce_whole_vocab and d % 128 == 0 and N % 8 == 0
-                and lce.grad_chunk(N, c.vocab_size) >= c.vocab_size):
-            keep = self._workspace("flce_keep", _lib.query("gptrig_flce_keep_bytes", N, c.vocab_size))
-        with self._timed("flce"):
-            if keep is not None:
-                _lib.call("gptrig_flce_fwd_keep", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
-                          lse_ce.data_ptr(), keep.data_ptr(), keep.numel(), ws.data_ptr(), ws.numel(), N, d,
-                          c.vocab_size, c.semantic_vocab_size, stream)
-            else:
+        dxf = torch.empty((N, d), dtype=BF16, device=self.device)
+        # Kept softmax: the forward keeps its probabilities (fp16 [vocab,
+        # chunk]) and the backward rescales them into the logit gradient
+        # instead of recomputing the logits GEMM; each token chunk runs its
+        # forward and backward back to back (bounded by vocab_tile_size unless
+        # flce_whole_vocab).  The head gradient accumulates over chunks.
+        chunk = flce_token_chunk(N, c.vocab_size, c.vocab_tile_size, c.flce_whole_vocab) \
+            if d % 128 == 0 and N % 8 == 0 else 0
+        if chunk:
+            keep = self._workspace("flce_keep", _lib.query("gptrig_flce_keep_bytes", chunk, c.vocab_size))
+            ws = self._workspace("flce_fwd", _lib.query("gptrig_flce_fwd_workspace_bytes", chunk, d, c.vocab_size))
+            ws_b = self._workspace("flce_bwd_keep", _lib.query("gptrig_flce_bwd_keep_workspace_bytes", chunk, d))
+            dw = A.grad(self.head_path)
+            with self._timed("flce"):
+                for c0 in range(0, N, chunk):
+                    n = min(chunk, N - c0)
+                    hp, tp = xf[c0:].data_ptr(), tgt[c0:].data_ptr()
+                    _lib.call("gptrig_flce_fwd_keep", hp, head.data_ptr(), tp, losses[c0:].data_ptr(),
+                              lse_ce[c0:].data_ptr(), keep.data_ptr(), keep.numel(), ws.data_ptr(), ws.numel(), n, d,
+                              c.vocab_size, c.semantic_vocab_size, stream)
+                    _lib.call("gptrig_flce_bwd_keep", hp, head.data_ptr(), tp, lse_ce[c0:].data_ptr(), None,
+                              loss_weight, dxf[c0:].data_ptr(), dw.data_ptr(), 1, keep.data_ptr(), keep.numel(),
+                              ws_b.data_ptr(), ws_b.numel(), n, d, c.vocab_size, c.semantic_vocab_size, stream)
+        else:
+            ws = self._workspace("flce_fwd", _lib.query("gptrig_flce_fwd_workspace_bytes", N, d, c.vocab_size))
+            with self._timed("flce"):
                 _lib.call("gptrig_flce_fwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), losses.data_ptr(),
                           lse_ce.data_ptr(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size,
                           stream)
@@ -509,23 +546,16 @@ class GPTTrainer:
                 self.loss.add_(aux * (c.router_aux_coefficient * c.experts / c.layers))
 
         # ---- backward ----
-        # One vocabulary chunk while the bf16 G^T fits the budget (6.6 GB at
-        # 65536 tokens x 50304), unless the config asks for the bounded tile.
-        dxf = torch.empty((N, d), dtype=BF16, device=self.device)
-        if keep is not None:
-            ws = self._workspace("flce_bwd_keep", _lib.query("gptrig_flce_bwd_keep_workspace_bytes", N, d))
-            with self._timed("flce"):
-                _lib.call("gptrig_flce_bwd_keep", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(),
-                          None, loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, keep.data_ptr(),
-                          keep.numel(), ws.data_ptr(), ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size, stream)
-        else:
-            chunk = lce.grad_chunk(N, c.vocab_size) if c.flce_whole_vocab else lce.chunk_for(c.vocab_tile_size)
+        if not chunk:
+            # (d not a multiple of 128) the recompute backward over vocabulary
+            # chunks of vocab_tile_size, or one chunk with flce_whole_vocab.
+            vchunk = lce.grad_chunk(N, c.vocab_size) if c.flce_whole_vocab else lce.chunk_for(c.vocab_tile_size)
             ws = self._workspace("flce_bwd",
-                                 _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, chunk))
+                                 _lib.query("gptrig_flce_bwd_workspace_bytes", N, d, c.vocab_size, vchunk))
             with self._timed("flce"):
                 _lib.call("gptrig_flce_bwd", xf.data_ptr(), head.data_ptr(), tgt.data_ptr(), lse_ce.data_ptr(), None,
                           loss_weight, dxf.data_ptr(), A.grad(self.head_path).data_ptr(), 1, ws.data_ptr(),
-                          ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size, chunk, stream)
+                          ws.numel(), N, d, c.vocab_size, c.semantic_vocab_size, vchunk, stream)
         unit = self.residual_scale == 1.0
         top = lin_dout[c.layers - 1]["mlp_down"] if unit and not c.experts else None
         dx, _ = rmsnorm_backward(dxf, x, A.w("final_ln_scale"), rstdf, A.grad("final_ln_scale"), True, out=top)

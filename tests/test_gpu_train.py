@@ -59,6 +59,57 @@ def test_train_step_history_matches_oracle(micro, embeddings, masking):
     assert np.all(np.abs(got[:, 2] - want[:, 2]) <= 2e-2 * want[:, 2])
 
 
+@pytest.mark.parametrize("label,model,trainer_only", [
+    ("kept softmax in 2 token chunks per micro-batch", dict(vocab_tile_size=256), {}),
+    ("kept softmax in one chunk", {}, dict(flce_whole_vocab=True)),
+    ("d_model 192: recompute over vocabulary chunks", dict(d_model=192, heads=3, vocab_tile_size=256), {}),
+])
+def test_train_step_flce_paths_match_oracle(label, model, trainer_only):
+    """The trainer's three FLCE wirings against the oracle's step: the
+    default kept softmax cut into token chunks by vocab_tile_size (256 here:
+    128-token chunks of the 256-token micro-batch), one chunk over all tokens
+    (flce_whole_vocab), and, for d_model not a multiple of 128, the forward
+    plus recompute backward over vocabulary chunks of vocab_tile_size."""
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer, flce_token_chunk
+
+    steps = 3
+    common = dict(layers=2, heads=2, d_model=128, vocab_size=1000, semantic_vocab_size=997, seq_len=128,
+                  batch_size=4, base_width=128, base_depth=2, attention_scale="inverse_sqrt_head_dim",
+                  embeddings="untied")
+    common.update(model)
+    opt = dict(learning_rate=2.0 ** -8, steps=steps, warmup_steps=1)
+    ocfg = om.Config(**common, attention_backend="flash", optimizer=oopt.OptimizerConfig(**opt))
+    gcfg = GPTConfig(**common, **trainer_only, micro_batch_size=2, optimizer=OptimizerConfig(**opt))
+    chunk = flce_token_chunk(256, 1000, gcfg.vocab_tile_size, gcfg.flce_whole_vocab)
+    print(f"train case {label}: token chunk {chunk}", flush=True)
+    if "token chunks" in label:
+        assert chunk == 128
+    windows = om.synthetic_windows(7, steps, 4, 128, 997)
+    state = om.init_state(ocfg, 0)
+    trainer = GPTTrainer(gcfg, seed=0)
+    for i in range(steps):
+        w = torch.from_numpy(windows[i])
+        om.train_step(state, w[:, :-1], w[:, 1:], ocfg)
+        trainer.train_step(w[:, :-1].cuda(), w[:, 1:].cuda())
+    got = trainer.history_rows()
+    want = np.asarray(state.history)
+    print("gpu   ", got.tolist(), flush=True)
+    print("oracle", want.tolist(), flush=True)
+    assert abs(got[0, 0] - want[0, 0]) <= 1e-3 * want[0, 0]
+    assert np.all(np.abs(got[:, 0] - want[:, 0]) <= 1e-2 * want[:, 0])
+    np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-6)
+    assert np.all(np.abs(got[:, 2] - want[:, 2]) <= 2e-2 * want[:, 2])
+    # The head's update carries the FLCE gradient directly.
+    init = om.flatten(om.init_params(ocfg, 0))
+    p0 = torch.from_numpy(np.asarray(init["output_embedding"]))
+    du = (trainer.arena.param("output_embedding").cpu() - p0).double().reshape(-1)
+    dw = (state.params["output_embedding"] - p0).double().reshape(-1)
+    ratio, cos = float(du.norm() / dw.norm()), float(du @ dw / (du.norm() * dw.norm()))
+    print(f"output_embedding update norm ratio {ratio:.4f}, cosine {cos:.4f}", flush=True)
+    assert abs(ratio - 1) <= 0.1 and cos >= 0.9
+
+
 def test_train_step_completep_clip_and_residual_scale_match_oracle():
     """The official parameterization (completep_fixed_tpp_v1, recipes/reference/
     config.yaml:22-30) at width multiplier 2 and depth multiplier 2 with
