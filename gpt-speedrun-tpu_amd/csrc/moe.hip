@@ -3,10 +3,11 @@
 // route_topk: one thread per token.  softmax over the fp32 router logits,
 //   jax.lax.top_k selection (largest value first; on equal values the lower
 //   expert index first), softmax over the chosen logits.
-// route_sort: one 1024-thread workgroup builds the dropless bucket layout:
-//   counts[e], and order = stable argsort(chosen.reshape(-1)) by counting sort
-//   (per-expert bases from an exclusive scan of counts, stable ranks from
-//   wave ballots in slot order), rows = order / top_k, position = order^-1.
+// route_hist / route_place build the dropless bucket layout over blocks of
+//   1024 slots: counts[e], and order = stable argsort(chosen.reshape(-1)) by
+//   counting sort (per-block counts in the workspace, per-expert bases from
+//   the totals and the blocks before, stable ranks within a block from wave
+//   ballots in slot order), rows = order / top_k, position = order^-1.
 //
 // The routed MLP around it (:1275-1293):
 //   router_logits   fp32 x @ router_w (one wave per token, weights in LDS);
@@ -20,7 +21,7 @@
 // gradients, split-K fp32 atomics), gather_bwd (the VJP of flat[rows]) and
 // router_bwd (gate/probability softmax VJPs, dx and d router_w).
 #include "common.h"
-#include "gemm_core.h"
+#include "epilogue.h"
 
 #include <math.h>
 
@@ -69,92 +70,144 @@ __global__ void route_topk_kernel(const float* __restrict__ logits, float* __res
   }
 }
 
-__global__ void __launch_bounds__(1024) route_sort_kernel(const int32_t* __restrict__ chosen, int n_slots, int E,
-                                                          int k, int32_t* __restrict__ counts,
-                                                          int32_t* __restrict__ order, int32_t* __restrict__ rows,
-                                                          int32_t* __restrict__ position) {
+// Stable bucket order over blocks of kSortBlock slots, in two launches.
+// route_hist: each block's per-expert counts into hist[block][e].  route_place:
+// each block finds its experts' bases (all experts' totals before e, plus
+// the counts of e in the blocks before it) and places its slots at base +
+// rank, the rank within the block from wave ballots in slot order; block 0
+// also writes counts.
+constexpr int kSortBlock = 1024;
+
+__global__ void __launch_bounds__(kSortBlock) route_hist_kernel(const int32_t* __restrict__ chosen, int n_slots,
+                                                                int E, int32_t* __restrict__ hist) {
   __shared__ int cnt[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int wave_cnt[16][kMaxExperts];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   if (tid < E) cnt[tid] = 0;
   __syncthreads();
-  for (int s = tid; s < n_slots; s += blockDim.x) atomicAdd(&cnt[chosen[s]], 1);
+  const int s = blockIdx.x * kSortBlock + tid;
+  if (s < n_slots) atomicAdd(&cnt[chosen[s]], 1);
+  __syncthreads();
+  if (tid < E) hist[(size_t)blockIdx.x * E + tid] = cnt[tid];
+}
+
+__global__ void __launch_bounds__(kSortBlock) route_place_kernel(const int32_t* __restrict__ chosen, int n_slots,
+                                                                 int E, int k, const int32_t* __restrict__ hist,
+                                                                 int nblocks, int32_t* __restrict__ counts,
+                                                                 int32_t* __restrict__ order, int32_t* __restrict__ rows,
+                                                                 int32_t* __restrict__ position) {
+  __shared__ int total[kMaxExperts], before[kMaxExperts], base[kMaxExperts];
+  __shared__ int wave_cnt[kSortBlock / 64][kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int blk = blockIdx.x;
+  if (tid < E) {
+    int tot = 0, bef = 0;
+    for (int b = 0; b < nblocks; ++b) {
+      const int h = hist[(size_t)b * E + tid];
+      tot += h;
+      bef += b < blk ? h : 0;
+    }
+    total[tid] = tot;
+    before[tid] = bef;
+    if (blk == 0) counts[tid] = tot;
+  }
   __syncthreads();
   if (tid == 0) {
     int acc = 0;
     for (int e = 0; e < E; ++e) {
-      base[e] = acc;
-      acc += cnt[e];
-      counts[e] = cnt[e];
+      base[e] = acc + before[e];
+      acc += total[e];
     }
   }
-  __syncthreads();
+  const int s = blk * kSortBlock + tid;
+  const int my_e = s < n_slots ? chosen[s] : -1;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int tile = 0; tile < n_slots; tile += blockDim.x) {
-    const int s = tile + tid;
-    const int my_e = s < n_slots ? chosen[s] : -1;
-    int rank = 0;
-    for (int e = 0; e < E; ++e) {
-      const uint64_t m = __ballot(my_e == e);
-      if (my_e == e) rank = __popcll(m & lt_mask);
-      if (lane == 0) wave_cnt[wave][e] = __popcll(m);
-    }
-    __syncthreads();
-    if (my_e >= 0) {
-      int before = 0;
-      for (int w = 0; w < wave; ++w) before += wave_cnt[w][my_e];
-      const int pos = base[my_e] + before + rank;
-      order[pos] = s;
-      rows[pos] = s / k;
-      if (position) position[s] = pos;
-    }
-    __syncthreads();
-    if (tid < E) {
-      int tot = 0;
-      for (int w = 0; w < 16; ++w) tot += wave_cnt[w][tid];
-      base[tid] += tot;
-    }
-    __syncthreads();
+  int rank = 0;
+  for (int e = 0; e < E; ++e) {
+    const uint64_t m = __ballot(my_e == e);
+    if (my_e == e) rank = __popcll(m & lt_mask);
+    if (lane == 0) wave_cnt[wave][e] = __popcll(m);
+  }
+  __syncthreads();
+  if (my_e >= 0) {
+    int bw = 0;
+    for (int w = 0; w < wave; ++w) bw += wave_cnt[w][my_e];
+    const int pos = base[my_e] + bw + rank;
+    order[pos] = s;
+    rows[pos] = s / k;
+    if (position) position[s] = pos;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Router logits (:1259-1264): logits[t][e] = sum_d f32(x[t][d]) * w[d][e].
-// Each wave owns kRouterTokens consecutive tokens; lane l holds d = l + 64i.
+// A wave takes 8 tokens at a time: lane = 8 token + g reads the token's
+// 16-byte chunks g, g + 8, ... (each 8-lane group reads 128 contiguous
+// bytes of one row), multiplies them by w rows from LDS, and the 8 lanes of
+// a token add their partial logits with three xor exchanges.
 // ---------------------------------------------------------------------------
 constexpr int kMaxRouterExperts = 16;
-constexpr int kRouterTokens = 16;
+constexpr int kRouterTokens = 16;  // tokens per wave (two passes of 8)
 constexpr int kMaxRouterWidth = 4096;
 
+// 8 bf16 of row x[t] from column d (d < D), zeros past D.
+__device__ __forceinline__ void load_x8(const bf16* __restrict__ row, int d, int D, float (&xv)[8]) {
+  if (d + 8 <= D && ((D & 7) == 0)) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + d);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = (float)v[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = d + j < D ? (float)row[d + j] : 0.f;
+  }
+}
+
+template <int EP>
 __global__ void __launch_bounds__(256) router_logits_kernel(const bf16* __restrict__ x, const float* __restrict__ w,
                                                             float* __restrict__ logits, int T, int D, int E) {
-  extern __shared__ float wsh[];  // [D][E]
-  for (int i = threadIdx.x; i < D * E; i += blockDim.x) wsh[i] = w[i];
+  extern __shared__ float wsh[];  // [D][EP], zero past E
+  for (int i = threadIdx.x; i < D * EP; i += blockDim.x) {
+    const int d = i / EP, e = i % EP;
+    wsh[i] = e < E ? w[(size_t)d * E + e] : 0.f;
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t0 = (blockIdx.x * 4 + wave) * kRouterTokens;
-  for (int tt = 0; tt < kRouterTokens; ++tt) {
-    const int t = t0 + tt;
-    if (t >= T) break;
-    float acc[kMaxRouterExperts];
+  const int tok = lane >> 3, g = lane & 7;
+  const int wt0 = (blockIdx.x * 4 + wave) * kRouterTokens;
+#pragma unroll 1
+  for (int pass = 0; pass < kRouterTokens / 8; ++pass) {
+    const int t = wt0 + 8 * pass + tok;
+    float acc[EP];
 #pragma unroll
-    for (int e = 0; e < kMaxRouterExperts; ++e) acc[e] = 0.f;
-    for (int d = lane; d < D; d += 64) {
-      const float xv = (float)x[(size_t)t * D + d];
+    for (int e = 0; e < EP; ++e) acc[e] = 0.f;
+    if (t < T) {
+      const bf16* row = x + (size_t)t * D;
+      for (int d = 8 * g; d < D; d += 64) {
+        float xv[8];
+        load_x8(row, d, D, xv);
 #pragma unroll
-      for (int e = 0; e < kMaxRouterExperts; ++e)
-        if (e < E) acc[e] = fmaf(xv, wsh[d * E + e], acc[e]);
-    }
-    float mine = 0.f;
+        for (int j = 0; j < 8; ++j) {
+          if (d + j >= D) break;
+          const float* wr = wsh + (d + j) * EP;
 #pragma unroll
-    for (int e = 0; e < kMaxRouterExperts; ++e) {
-      if (e < E) {
-        const float v = wave_sum(acc[e]);
-        if (lane == e) mine = v;
+          for (int e4 = 0; e4 < EP; e4 += 4) {
+            const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr + e4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[e4 + u] = fmaf(xv[j], w4[u], acc[e4 + u]);
+          }
+        }
       }
     }
-    if (lane < E) logits[(size_t)t * E + lane] = mine;
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+      acc[e] += __shfl_xor(acc[e], 1);
+      acc[e] += __shfl_xor(acc[e], 2);
+      acc[e] += __shfl_xor(acc[e], 4);
+    }
+    if (t < T) {
+#pragma unroll
+      for (int e = 0; e < EP; ++e)
+        if (e % 8 == g && e < E) logits[(size_t)t * E + e] = acc[e];
+    }
   }
 }
 
@@ -164,6 +217,9 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const bf16* __restri
 // A K-major [R][K] (rows in bucket order), B_e either [K][N]
 // (kBT = false: rhs + e*K*N) or [N][K] (kBT = true: the transpose, for dX).
 // Grid: (ceil(R/256) + E) M-tile slots x ceil(N/256); surplus slots exit.
+// Each 256 x 256 tile is computed transposed (features x bucket rows) and
+// written through LDS in whole rows by the shared epilogue (epilogue.h),
+// which also reads pre in whole rows for kMode 2.
 // kMode 0: out = bf16(acc) (+ bias)
 //       1: pre = bf16(bf16(acc) + bias), out = bf16(gelu(pre))
 //       2: out = bf16(bf16(acc) * gelu'(pre))   (pre read, same layout as out)
@@ -173,9 +229,10 @@ __global__ void __launch_bounds__(gemm::THREADS)
     moe_gmm_kernel(const bf16* __restrict__ lhs, int64_t lda,
                    const bf16* __restrict__ rhs, const int32_t* __restrict__ counts, int E, int K, int N,
                    const bf16* __restrict__ bias, bf16* __restrict__ out, bf16* __restrict__ pre, int64_t ldo) {
+  __shared__ __attribute__((aligned(16))) float bias_s[gemm::BM];
   const int ntn = (N + gemm::BN - 1) / gemm::BN;
-  const int tn = blockIdx.x % ntn;
-  int tm = blockIdx.x / ntn;
+  const int tn = blockIdx.x % ntn;  // feature tile
+  int tm = blockIdx.x / ntn;        // bucket-row tile of expert e
   int e = 0, off = 0;
   for (; e < E; ++e) {
     const int c = counts[e];
@@ -186,37 +243,28 @@ __global__ void __launch_bounds__(gemm::THREADS)
   }
   if (e >= E) return;  // uniform: surplus slot
   const int cnt = counts[e];
-  gemm::Operand A{lhs + (int64_t)off * lda, lda};
-  gemm::Operand B = kBT ? gemm::Operand{rhs + (int64_t)e * N * K, K} : gemm::Operand{rhs + (int64_t)e * K * N, N};
+  // The tile is computed transposed (rows = output features, columns =
+  // bucket rows), so it leaves through the shared token-row epilogue:
+  // A = the expert's weight (K-major [N][K] when transposed, else MN-major
+  // [K][N]), B = the bucket's rows (K-major).
+  const gemm::Operand Wop = kBT ? gemm::Operand{rhs + (int64_t)e * N * K, K} : gemm::Operand{rhs + (int64_t)e * K * N, N};
+  const gemm::Operand Xop{lhs + (int64_t)off * lda, lda};
+  constexpr int kEpi = kMode == 0 ? gemm_epi::kBias : kMode == 1 ? gemm_epi::kGelu : gemm_epi::kDGelu;
+  if constexpr (gemm_epi::has_bias(kEpi)) gemm_epi::stage_bias(bias_s, bias ? bias + (int64_t)e * N : nullptr, tn * gemm::BM, N);
   f32x16 acc[4][2];
-  gemm::mainloop_pp<true, kBT>(acc, A, B, cnt, N, 0, K, tm * gemm::BM, tn * gemm::BN);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5, l32 = lane & 31;
-  const int wm = wave & 1, wn = wave >> 1;
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int n = tn * gemm::BN + 64 * wn + 32 * nb + l32;
-    if (n >= N) continue;
-    const float bv = bias ? (float)bias[(int64_t)e * N + n] : 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = tm * gemm::BM + 128 * wm + 32 * mb + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (m >= cnt) continue;
-        const int64_t o = (int64_t)(off + m) * ldo + n;
-        const float g = (float)(bf16)acc[mb][nb][i];
-        if (kMode == 0) {
-          out[o] = bias ? (bf16)(g + bv) : (bf16)g;
-        } else if (kMode == 1) {
-          const bf16 h = (bf16)(g + bv);
-          pre[o] = h;
-          out[o] = (bf16)gelu_f((float)h);
-        } else {
-          out[o] = (bf16)(g * gelu_grad_f((float)pre[o]));
-        }
-      }
+  gemm::mainloop_pp<kBT, true>(acc, Wop, Xop, N, cnt, 0, K, tn * gemm::BM, tm * gemm::BN);
+  gemm_epi::EpiArgs ea{};
+  const int64_t base = (int64_t)off * ldo;
+  if (kMode == 1) {
+    ea.y = pre + base;  // h = bf16(bf16(acc) + b)
+    ea.act = out + base;  // gelu(h)
+  } else {
+    ea.y = out + base;
   }
+  ea.ldy = ldo;
+  ea.aux = kMode == 2 ? pre + base : nullptr;
+  ea.ldaux = ldo;
+  gemm_epi::linear_epilogue<kEpi>(acc, tn, tm, N, cnt, ea, bias_s);
 }
 
 // Per-expert weight (+ bias) gradients:
@@ -378,35 +426,42 @@ __global__ void __launch_bounds__(256) moe_gather_bwd_kernel(const bf16* __restr
   }
 }
 
-// Router statistics (:1295-1306), one 1024-thread workgroup:
-// mean_probability[e] = mean_t probs[t][e]; load[e] = counts[e] / (T*k);
-// summary = (mean_t entropy_t, mean_t max_j gate[t][j], sqrt(mean logits^2)).
-__global__ void __launch_bounds__(1024) moe_stats_kernel(const float* __restrict__ logits, const float* __restrict__ probs,
-                                                         const float* __restrict__ gate, const int32_t* __restrict__ counts,
-                                                         int T, int E, int k, float* __restrict__ mean_probability,
-                                                         float* __restrict__ load, float* __restrict__ summary) {
-  __shared__ float red[3 + kMaxExperts][16];
+// Router statistics (:1295-1306): the sums of probabilities, entropies,
+// top-1 gates and squared logits over the tokens, in three launches:
+// stats_zero clears the outputs, moe_stats_kernel (one thread per token)
+// adds each workgroup's sums into them with atomics, stats_finalize divides
+// (and takes the root of the mean square) and writes the load.
+__global__ void stats_zero_kernel(float* __restrict__ mean_probability, float* __restrict__ summary, int E) {
+  const int i = threadIdx.x;
+  if (i < E) mean_probability[i] = 0.f;
+  if (i < 3) summary[i] = 0.f;
+}
+
+template <int EP>
+__global__ void __launch_bounds__(256) moe_stats_kernel(const float* __restrict__ logits, const float* __restrict__ probs,
+                                                        const float* __restrict__ gate, int T, int E, int k,
+                                                        float* __restrict__ mean_probability,
+                                                        float* __restrict__ summary) {
+  __shared__ float red[3 + EP][4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float pe[kMaxRouterExperts];
+  const int t = blockIdx.x * blockDim.x + tid;
+  float pe[EP], ent = 0.f, top = 0.f, sq = 0.f;
 #pragma unroll
-  for (int e = 0; e < kMaxRouterExperts; ++e) pe[e] = 0.f;
-  float ent = 0.f, top = 0.f, sq = 0.f;
-  for (int t = tid; t < T; t += blockDim.x) {
-    float h = 0.f;
+  for (int e = 0; e < EP; ++e) pe[e] = 0.f;
+  if (t < T) {
 #pragma unroll
-    for (int e = 0; e < kMaxRouterExperts; ++e) {
+    for (int e = 0; e < EP; ++e) {
       if (e < E) {
         const float pv = probs[(size_t)t * E + e];
         const float lv = logits[(size_t)t * E + e];
-        pe[e] += pv;
-        h -= pv * logf(pv + 1.0e-9f);
+        pe[e] = pv;
+        ent -= pv * logf(pv + 1.0e-9f);
         sq = fmaf(lv, lv, sq);
       }
     }
-    ent += h;
     float gm = gate[(size_t)t * k];
     for (int j = 1; j < k; ++j) gm = fmaxf(gm, gate[(size_t)t * k + j]);
-    top += gm;
+    top = gm;
   }
   float vals[3] = {ent, top, sq};
 #pragma unroll
@@ -415,7 +470,7 @@ __global__ void __launch_bounds__(1024) moe_stats_kernel(const float* __restrict
     if (lane == 0) red[q][wave] = v;
   }
 #pragma unroll
-  for (int e = 0; e < kMaxRouterExperts; ++e) {
+  for (int e = 0; e < EP; ++e) {
     if (e < E) {
       const float v = wave_sum(pe[e]);
       if (lane == 0) red[3 + e][wave] = v;
@@ -423,77 +478,163 @@ __global__ void __launch_bounds__(1024) moe_stats_kernel(const float* __restrict
   }
   __syncthreads();
   if (tid < 3 + E) {
-    float s = 0.f;
-    for (int w = 0; w < 16; ++w) s += red[tid][w];
-    if (tid == 0) summary[0] = s / T;
-    else if (tid == 1) summary[1] = s / T;
-    else if (tid == 2) summary[2] = sqrtf(s / ((float)T * E));
-    else mean_probability[tid - 3] = s / T;
+    const float v = red[tid][0] + red[tid][1] + red[tid][2] + red[tid][3];
+    atomicAdd(tid < 3 ? summary + tid : mean_probability + (tid - 3), v);
   }
-  if (tid < E) load[tid] = (float)counts[tid] / (float)((long long)T * k);
 }
 
-// Router backward, per token t (one wave per kRouterTokens tokens):
+__global__ void stats_finalize_kernel(const int32_t* __restrict__ counts, int T, int E, int k,
+                                      float* __restrict__ mean_probability, float* __restrict__ load,
+                                      float* __restrict__ summary) {
+  const int i = threadIdx.x;
+  if (i < E) {
+    mean_probability[i] = mean_probability[i] / T;
+    load[i] = (float)counts[i] / (float)((long long)T * k);
+  }
+  if (i == 0) {
+    summary[0] = summary[0] / T;
+    summary[1] = summary[1] / T;
+    summary[2] = sqrtf(summary[2] / ((float)T * E));
+  }
+}
+
+// Router backward, per token t:
 //   dchosen[j] = gate[j] * (dgate[j] - sum_i gate[i] dgate[i])        (gate softmax)
 //   dprobs[e]  = dmean_probability[e] / T                              (mean over tokens)
 //   dlogits[e] = probs[e] * (dprobs[e] - sum_i probs[i] dprobs[i]) + sum_{j: chosen[j]=e} dchosen[j]
 //   dx[t][d]   = bf16(dx[t][d] + bf16(sum_e dlogits[e] w[d][e]))       (in place)
-//   dw[d][e]  += sum_t f32(x[t][d]) dlogits[e]                         (fp32 atomics per workgroup)
+//   dw[d][e]  += sum_t f32(x[t][d]) dlogits[e]
+// A workgroup takes a tile of kRouterBwdCols width columns x
+// kRouterBwdTokens tokens.  Its threads first turn each token's gate and
+// probability cotangents into dlogits (LDS); then thread (token lane tl,
+// chunk c) walks tokens tl, tl + 32, ... for the 8 columns 8 c .. 8 c + 7 of
+// the tile: dx[t][chunk] += bf16(dlogits[t] @ w[chunk]^T) (a 16-byte
+// read-modify-write; the 8 chunk threads of a token cover 128 contiguous
+// bytes) and the chunk's dw partial f32 [8][EP] in registers.  The 32 token
+// lanes' partials are summed with xor exchanges and through LDS, and each
+// workgroup adds one value per (column, expert) to dw with an atomic.
+constexpr int kRouterBwdTokens = 1024;
+constexpr int kRouterBwdCols = 64;
+
+template <int EP>
 __global__ void __launch_bounds__(256) router_bwd_kernel(const bf16* __restrict__ x, const float* __restrict__ w,
                                                          const float* __restrict__ probs, const int32_t* __restrict__ chosen,
                                                          const float* __restrict__ gate, const float* __restrict__ dgate,
                                                          const float* __restrict__ dmean_probability,
                                                          bf16* __restrict__ dx, float* __restrict__ dw, int T, int D,
                                                          int E, int k) {
-  extern __shared__ float smem[];
-  float* wsh = smem;           // [D][E]
-  float* dwsh = smem + D * E;  // [D][E] workgroup partial of dw
-  for (int i = threadIdx.x; i < D * E; i += blockDim.x) {
-    wsh[i] = w[i];
-    dwsh[i] = 0.f;
+  __shared__ __attribute__((aligned(16))) float dl_s[kRouterBwdTokens][EP];
+  __shared__ float red[4][kRouterBwdCols][EP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tb = blockIdx.y * kRouterBwdTokens;
+  const int col0 = blockIdx.x * kRouterBwdCols;
+  for (int i = tid; i < kRouterBwdTokens; i += blockDim.x) {
+    const int t = tb + i;
+    float dl[EP];
+#pragma unroll
+    for (int e = 0; e < EP; ++e) dl[e] = 0.f;
+    if (t < T) {
+      if (dmean_probability) {
+        float pd = 0.f;
+#pragma unroll
+        for (int e = 0; e < EP; ++e)
+          if (e < E) pd += probs[(size_t)t * E + e] * (dmean_probability[e] / T);
+#pragma unroll
+        for (int e = 0; e < EP; ++e)
+          if (e < E) dl[e] = probs[(size_t)t * E + e] * (dmean_probability[e] / T - pd);
+      }
+      float gd = 0.f;
+      for (int j = 0; j < k; ++j) gd += gate[(size_t)t * k + j] * dgate[(size_t)t * k + j];
+      for (int j = 0; j < k; ++j) {
+        const float dc = gate[(size_t)t * k + j] * (dgate[(size_t)t * k + j] - gd);
+        const int ce = chosen[(size_t)t * k + j];
+#pragma unroll
+        for (int e = 0; e < EP; ++e)
+          if (e == ce) dl[e] += dc;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EP; ++e) dl_s[i][e] = dl[e];
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t0 = (blockIdx.x * 4 + wave) * kRouterTokens;
-  for (int tt = 0; tt < kRouterTokens; ++tt) {
-    const int t = t0 + tt;
-    if (t >= T) break;
-    // dlogits for this token, computed redundantly by every lane (E <= 16).
-    float dl[kMaxRouterExperts];
-    float pd = 0.f;
+  const int c = tid & 7, tl = tid >> 3;  // chunk of the tile, token lane (0 .. 31)
+  const int d0 = col0 + 8 * c;
+  const bool vec = (D & 7) == 0 && d0 + 8 <= D;
+  float wc[8][EP], dwp[8][EP];
 #pragma unroll
-    for (int e = 0; e < kMaxRouterExperts; ++e) {
-      dl[e] = 0.f;
-      if (e < E && dmean_probability) pd += probs[(size_t)t * E + e] * (dmean_probability[e] / T);
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+      wc[j][e] = (d0 + j < D && e < E) ? w[(size_t)(d0 + j) * E + e] : 0.f;
+      dwp[j][e] = 0.f;
     }
+  if (d0 < D) {
+    for (int i = tl; i < kRouterBwdTokens; i += 32) {
+      const int t = tb + i;
+      if (t >= T) break;
+      const bf16* xrow = x + (size_t)t * D + d0;
+      bf16* drow = dx + (size_t)t * D + d0;
+      float xv[8], old[8];
+      if (vec) {
+        const bf16x8 xx = *reinterpret_cast<const bf16x8*>(xrow);
+        const bf16x8 dd = *reinterpret_cast<const bf16x8*>(drow);
 #pragma unroll
-    for (int e = 0; e < kMaxRouterExperts; ++e)
-      if (e < E && dmean_probability) dl[e] = probs[(size_t)t * E + e] * (dmean_probability[e] / T - pd);
-    float gd = 0.f;
-    for (int j = 0; j < k; ++j) gd += gate[(size_t)t * k + j] * dgate[(size_t)t * k + j];
-    for (int j = 0; j < k; ++j) {
-      const float dc = gate[(size_t)t * k + j] * (dgate[(size_t)t * k + j] - gd);
-      const int ce = chosen[(size_t)t * k + j];
+        for (int j = 0; j < 8; ++j) {
+          xv[j] = (float)xx[j];
+          old[j] = (float)dd[j];
+        }
+      } else {
 #pragma unroll
-      for (int e = 0; e < kMaxRouterExperts; ++e)
-        if (e == ce) dl[e] += dc;
-    }
-    for (int d = lane; d < D; d += 64) {
-      const float xv = (float)x[(size_t)t * D + d];
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < kMaxRouterExperts; ++e) {
-        if (e < E) {
-          s = fmaf(dl[e], wsh[d * E + e], s);
-          atomicAdd(&dwsh[d * E + e], xv * dl[e]);  // LDS atomic: waves of the workgroup share d
+        for (int j = 0; j < 8; ++j) {
+          xv[j] = d0 + j < D ? (float)xrow[j] : 0.f;
+          old[j] = d0 + j < D ? (float)drow[j] : 0.f;
         }
       }
-      const size_t o = (size_t)t * D + d;
-      dx[o] = (bf16)((float)dx[o] + (float)(bf16)s);
+      float dl[EP];
+#pragma unroll
+      for (int e4 = 0; e4 < EP; e4 += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&dl_s[i][e4]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dl[e4 + u] = v[u];
+      }
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float sj = 0.f;
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+          sj = fmaf(dl[e], wc[j][e], sj);
+          dwp[j][e] = fmaf(xv[j], dl[e], dwp[j][e]);
+        }
+        o[j] = (bf16)(old[j] + (float)(bf16)sj);
+      }
+      if (vec) {
+        *reinterpret_cast<bf16x8*>(drow) = o;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (d0 + j < D) drow[j] = o[j];
+      }
     }
   }
+  // Sum the token lanes: lanes 8 m + c of a wave (m = 0..7) by xor over
+  // lane bits 3..5, then the 4 waves through LDS.
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+      float v = dwp[j][e];
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (lane < 8) red[wave][8 * c + j][e] = v;
+    }
   __syncthreads();
-  for (int i = threadIdx.x; i < D * E; i += blockDim.x) atomicAdd(dw + i, dwsh[i]);
+  for (int i = tid; i < kRouterBwdCols * EP; i += blockDim.x) {
+    const int col = i / EP, e = i % EP;
+    const float v = red[0][col][e] + red[1][col][e] + red[2][col][e] + red[3][col][e];
+    if (col0 + col < D && e < E) atomicAdd(dw + (size_t)(col0 + col) * E + e, v);
+  }
 }
 
 }  // namespace
@@ -501,24 +642,29 @@ __global__ void __launch_bounds__(256) router_bwd_kernel(const bf16* __restrict_
 extern "C" {
 
 size_t gptrig_moe_route_workspace_bytes(int tokens, int experts, int top_k) {
-  (void)tokens;
-  (void)experts;
-  (void)top_k;
-  return 0;
+  if (tokens <= 0 || experts <= 0 || top_k <= 0) return 0;
+  const size_t blocks = (size_t)ceil_div((int64_t)tokens * top_k, kSortBlock);
+  return (blocks * experts * sizeof(int32_t) + 255) & ~(size_t)255;
 }
 
 int gptrig_moe_route(const float* logits, float* probs, int32_t* chosen, float* gate, int32_t* counts,
                      int32_t* order, int32_t* rows, int32_t* position, void* workspace, size_t workspace_bytes,
                      int tokens, int experts, int top_k, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (!logits || !chosen || !gate || !counts || !order || !rows) return GPTRIG_E_NULL;
   if (tokens <= 0 || experts <= 0 || top_k <= 0) return GPTRIG_E_SHAPE;
   if (experts > kMaxExperts || top_k > experts) return GPTRIG_E_UNSUPPORTED;
+  if ((int64_t)tokens * top_k >= (1ll << 31)) return GPTRIG_E_SHAPE;
+  if (!workspace || workspace_bytes < gptrig_moe_route_workspace_bytes(tokens, experts, top_k))
+    return GPTRIG_E_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   route_topk_kernel<<<ceil_div(tokens, 128), 128, 0, s>>>(logits, probs, chosen, gate, tokens, experts, top_k);
   GPTRIG_CHECK_LAUNCH();
-  route_sort_kernel<<<1, 1024, 0, s>>>(chosen, tokens * top_k, experts, top_k, counts, order, rows, position);
+  const int n_slots = tokens * top_k, nblocks = ceil_div(n_slots, kSortBlock);
+  int32_t* hist = (int32_t*)workspace;
+  route_hist_kernel<<<nblocks, kSortBlock, 0, s>>>(chosen, n_slots, experts, hist);
+  GPTRIG_CHECK_LAUNCH();
+  route_place_kernel<<<nblocks, kSortBlock, 0, s>>>(chosen, n_slots, experts, top_k, hist, nblocks, counts, order,
+                                                    rows, position);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
@@ -529,9 +675,17 @@ int gptrig_moe_router_logits(const void* x, const float* router_w, float* logits
   if (!x || !router_w || !logits) return GPTRIG_E_NULL;
   if (tokens <= 0 || width <= 0 || experts <= 0) return GPTRIG_E_SHAPE;
   if (experts > kMaxRouterExperts || (size_t)width * experts * sizeof(float) > 32768) return GPTRIG_E_UNSUPPORTED;
-  const size_t smem = (size_t)width * experts * sizeof(float);
-  router_logits_kernel<<<ceil_div(tokens, 4 * kRouterTokens), 256, smem, (hipStream_t)stream>>>(
-      (const bf16*)x, router_w, logits, tokens, width, experts);
+  const int ep = experts <= 4 ? 4 : experts <= 8 ? 8 : 16;
+  if ((size_t)width * ep * sizeof(float) > 65536) return GPTRIG_E_UNSUPPORTED;
+  const size_t smem = (size_t)width * ep * sizeof(float);
+  const unsigned grid = (unsigned)ceil_div(tokens, 4 * kRouterTokens);
+  hipStream_t s = (hipStream_t)stream;
+  if (ep == 4)
+    router_logits_kernel<4><<<grid, 256, smem, s>>>((const bf16*)x, router_w, logits, tokens, width, experts);
+  else if (ep == 8)
+    router_logits_kernel<8><<<grid, 256, smem, s>>>((const bf16*)x, router_w, logits, tokens, width, experts);
+  else
+    router_logits_kernel<16><<<grid, 256, smem, s>>>((const bf16*)x, router_w, logits, tokens, width, experts);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
@@ -552,8 +706,8 @@ int gptrig_moe_gmm(const void* lhs, int64_t lda, const void* rhs, int rhs_transp
   if (!lhs || !rhs || !counts || !out) return GPTRIG_E_NULL;
   if ((mode == 1 || mode == 2) && !pre) return GPTRIG_E_NULL;
   if (rows <= 0 || k <= 0 || n <= 0 || experts <= 0 || mode < 0 || mode > 2) return GPTRIG_E_SHAPE;
-  if (k % 8 || n % 8 || lda % 8 || lda < k || ldo < n) return GPTRIG_E_SHAPE;
-  if (((uintptr_t)lhs | (uintptr_t)rhs) & 15) return GPTRIG_E_SHAPE;
+  if (k % 8 || n % 8 || lda % 8 || lda < k || ldo < n || ldo % 8) return GPTRIG_E_SHAPE;
+  if (((uintptr_t)lhs | (uintptr_t)rhs | (uintptr_t)out | (uintptr_t)pre) & 15) return GPTRIG_E_SHAPE;
   if (experts > kMaxExperts) return GPTRIG_E_UNSUPPORTED;
   const unsigned grid = (unsigned)((ceil_div(rows, gemm::BM) + experts) * ceil_div(n, gemm::BN));
   hipStream_t s = (hipStream_t)stream;
@@ -631,8 +785,18 @@ int gptrig_moe_stats(const float* logits, const float* probs, const float* gate,
   if (!logits || !probs || !gate || !counts || !mean_probability || !load || !summary) return GPTRIG_E_NULL;
   if (tokens <= 0 || experts <= 0 || top_k <= 0 || top_k > experts) return GPTRIG_E_SHAPE;
   if (experts > kMaxRouterExperts) return GPTRIG_E_UNSUPPORTED;
-  moe_stats_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(logits, probs, gate, counts, tokens, experts, top_k,
-                                                        mean_probability, load, summary);
+  hipStream_t s = (hipStream_t)stream;
+  stats_zero_kernel<<<1, 64, 0, s>>>(mean_probability, summary, experts);
+  GPTRIG_CHECK_LAUNCH();
+  const unsigned grid = (unsigned)ceil_div(tokens, 256);
+  if (experts <= 4)
+    moe_stats_kernel<4><<<grid, 256, 0, s>>>(logits, probs, gate, tokens, experts, top_k, mean_probability, summary);
+  else if (experts <= 8)
+    moe_stats_kernel<8><<<grid, 256, 0, s>>>(logits, probs, gate, tokens, experts, top_k, mean_probability, summary);
+  else
+    moe_stats_kernel<16><<<grid, 256, 0, s>>>(logits, probs, gate, tokens, experts, top_k, mean_probability, summary);
+  GPTRIG_CHECK_LAUNCH();
+  stats_finalize_kernel<<<1, 64, 0, s>>>(counts, tokens, experts, top_k, mean_probability, load, summary);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
@@ -643,10 +807,17 @@ int gptrig_moe_router_bwd(const void* x, const float* router_w, const float* pro
   if (!x || !router_w || !probs || !chosen || !gate || !dgate || !dx || !dw_router) return GPTRIG_E_NULL;
   if (tokens <= 0 || width <= 0 || experts <= 0 || top_k <= 0 || top_k > experts) return GPTRIG_E_SHAPE;
   if (experts > kMaxRouterExperts || (size_t)width * experts * sizeof(float) > 32768) return GPTRIG_E_UNSUPPORTED;
-  const size_t smem = 2 * (size_t)width * experts * sizeof(float);
-  router_bwd_kernel<<<ceil_div(tokens, 4 * kRouterTokens), 256, smem, (hipStream_t)stream>>>(
-      (const bf16*)x, router_w, probs, chosen, gate, dgate, dmean_probability, (bf16*)dx, dw_router, tokens, width,
-      experts, top_k);
+  const dim3 grid((unsigned)ceil_div(width, kRouterBwdCols), (unsigned)ceil_div(tokens, kRouterBwdTokens));
+  hipStream_t s = (hipStream_t)stream;
+  if (experts <= 4)
+    router_bwd_kernel<4><<<grid, 256, 0, s>>>((const bf16*)x, router_w, probs, chosen, gate, dgate, dmean_probability,
+                                              (bf16*)dx, dw_router, tokens, width, experts, top_k);
+  else if (experts <= 8)
+    router_bwd_kernel<8><<<grid, 256, 0, s>>>((const bf16*)x, router_w, probs, chosen, gate, dgate, dmean_probability,
+                                              (bf16*)dx, dw_router, tokens, width, experts, top_k);
+  else
+    router_bwd_kernel<16><<<grid, 256, 0, s>>>((const bf16*)x, router_w, probs, chosen, gate, dgate,
+                                               dmean_probability, (bf16*)dx, dw_router, tokens, width, experts, top_k);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }

@@ -32,9 +32,10 @@ def _route(flat: torch.Tensor, router_w: torch.Tensor, experts: int, top_k: int)
     order = torch.empty(tokens * top_k, dtype=torch.int32, device=dev)
     rows = torch.empty(tokens * top_k, dtype=torch.int32, device=dev)
     position = torch.empty(tokens * top_k, dtype=torch.int32, device=dev)
+    ws = _lib.workspace(_lib.query("gptrig_moe_route_workspace_bytes", tokens, experts, top_k), dev)
     _lib.call("gptrig_moe_route", logits.data_ptr(), probs.data_ptr(), chosen.data_ptr(), gate.data_ptr(),
-              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), None, 0, tokens, experts,
-              top_k, s)
+              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), ws.data_ptr(), ws.numel(),
+              tokens, experts, top_k, s)
     return logits, probs, chosen, gate, counts, rows, position
 
 

@@ -349,8 +349,10 @@ class GPTTrainer:
         order = torch.empty(R, dtype=torch.int32, device=dev)
         rows = torch.empty(R, dtype=torch.int32, device=dev)
         position = torch.empty(R, dtype=torch.int32, device=dev)
+        ws = self._workspace("moe_route", _lib.query("gptrig_moe_route_workspace_bytes", N, E, k))
         _lib.call("gptrig_moe_route", logits.data_ptr(), probs.data_ptr(), chosen.data_ptr(), gate.data_ptr(),
-                  counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), None, 0, N, E, k, s)
+                  counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), ws.data_ptr(), ws.numel(),
+                  N, E, k, s)
         grouped = torch.empty((R, d), dtype=BF16, device=dev)
         _lib.call("gptrig_moe_gather_rows", xn2.data_ptr(), rows.data_ptr(), grouped.data_ptr(), R, d, s)
         pre = torch.empty((R, eh), dtype=BF16, device=dev)

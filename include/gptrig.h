@@ -130,12 +130,14 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
  * tile from the saved (hidden, weight) (rig/kernels/linear_cross_entropy.py:
  * 220-302); this pair instead keeps the forward's probabilities for the
  * backward, as fp16 exp(logit - m) with m the max over 128 vocabulary rows,
- * plus m: a [vocab, n] 16-bit array, so a caller that can hold it (the
- * trainer's whole-vocabulary opt-in, 6.6 GB at 65536 tokens) trades the
- * recompute GEMM for two bandwidth passes.  Same losses and lse as
- * gptrig_flce_fwd; gradient values as gptrig_flce_bwd's up to one fp16
- * rounding of each probability before its bf16 rounding.  d a multiple of 128 and n of 8 (else
- * GPTRIG_E_UNSUPPORTED).  keep: gptrig_flce_keep_bytes(n, vocab) bytes, 16-byte
+ * plus m: a [vocab, n] 16-bit array, so a caller that can hold it trades
+ * the recompute GEMM for two bandwidth passes.  The trainer calls the pair
+ * on token chunks sized so the array stays within the reference's fp32
+ * [tokens, vocab_tile_size] logits (or on all tokens at once, 6.6 GB at
+ * 65536, when asked for the whole vocabulary), accumulating dweight.  Same
+ * losses and lse as gptrig_flce_fwd; gradient values as gptrig_flce_bwd's up
+ * to one fp16 rounding of each probability before its bf16 rounding.  d a
+ * multiple of 128 and n of 8 (else GPTRIG_E_UNSUPPORTED).  keep: gptrig_flce_keep_bytes(n, vocab) bytes, 16-byte
  * aligned, written by the forward and consumed (overwritten) by the backward,
  * which must see the forward's lse.  The backward's workspace is the f32
  * [n, d] dh accumulator. */

@@ -11,9 +11,16 @@ float32 summation order, and this trajectory is chaotic enough around its
 loss spike (steps 4-9) that the same code on 8 threads differs by about 0.5%
 at step 8 (``make_trajectory_perturbed.py eight_threads``).
 
-Usage: ``python tests/golden/make_trajectory.py`` (about 12 minutes).
-Output: ``tests/golden/config_a_trajectory.json`` with one
-(loss, learning_rate, grad_norm) row per step.
+A second schedule, ``long_warmup``, warms the learning rate up over all 20
+steps (2^-8 reached at step 20) instead of 2: its run has no loss spike, and
+the reference-equivalent variations of ``make_trajectory_perturbed.py`` stay
+within 0.1% of it at every step, so a GPU run can be held to 1% of this
+fixture alone.
+
+Usage: ``python tests/golden/make_trajectory.py [long_warmup]`` (about 12
+minutes).  Output: ``tests/golden/config_a_trajectory.json`` (or
+``config_a_long_warmup_trajectory.json``) with one (loss, learning_rate,
+grad_norm) row per step.
 """
 
 from __future__ import annotations
@@ -35,9 +42,30 @@ SEED = 0
 THREADS = 3
 
 
-def main() -> None:
-    torch.set_num_threads(THREADS)
+SCHEDULES = {"spike": None, "long_warmup": STEPS}  # warmup steps (None: the config's 10%)
+
+
+def schedule_config(schedule: str):
+    """Config A with the named learning-rate warmup."""
+
+    from dataclasses import replace
+
     config = om.baseline_config("A", steps=STEPS)
+    warmup = SCHEDULES[schedule]
+    if warmup is not None:
+        config = replace(config, optimizer=replace(config.optimizer, warmup_steps=warmup))
+    return config
+
+
+def fixture_name(schedule: str, variation: str = "") -> str:
+    stem = "config_a_trajectory" if schedule == "spike" else f"config_a_{schedule}_trajectory"
+    return f"{stem}_{variation}.json" if variation else f"{stem}.json"
+
+
+def main() -> None:
+    schedule = sys.argv[1] if len(sys.argv) > 1 else "spike"
+    torch.set_num_threads(THREADS)
+    config = schedule_config(schedule)
     windows = om.synthetic_windows(SEED, STEPS, config.batch_size, config.seq_len, config.vocab_size)
     state = om.init_state(config, SEED)
     rows = []
@@ -48,13 +76,14 @@ def main() -> None:
         rows.append([rec["loss"], rec["learning_rate"], rec["grad_norm"]])
         print(f"step {i + 1}: {rows[-1]} ({time.time() - t0:.1f} s)", flush=True)
     out = {
-        "config": "A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup 2 cosine, 20 steps",
+        "config": (f"A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup "
+                   f"{config.optimizer.warmup_steps} cosine, 20 steps"),
         "seed": SEED,
         "windows": "numpy default_rng(0).integers(0, 50304, (20, 8, 1025), int32)",
         "columns": ["loss", "learning_rate", "grad_norm"],
         "rows": rows,
     }
-    with open(os.path.join(HERE, "config_a_trajectory.json"), "w") as f:
+    with open(os.path.join(HERE, fixture_name(schedule)), "w") as f:
         json.dump(out, f, indent=1)
 
 

@@ -20,9 +20,10 @@ windows) except for one of:
 * ``eight_threads``: nothing but the CPU thread count (8 instead of the
   fixture's 3), which changes torch's float32 summation order.
 
-Usage: ``python tests/golden/make_trajectory_perturbed.py f64_linear|dense_attention|normalized_attention|eight_threads``
-(10-40 minutes on 8 cores).  Output:
-``tests/golden/config_a_trajectory_<variation>.json``.
+Usage: ``python tests/golden/make_trajectory_perturbed.py f64_linear|dense_attention|normalized_attention|eight_threads
+[spike|long_warmup]`` (10-40 minutes on 8 cores).  Output:
+``tests/golden/config_a_trajectory_<variation>.json`` (``config_a_long_warmup_trajectory_<variation>.json``
+for the second schedule, see ``make_trajectory.py``).
 """
 
 from __future__ import annotations
@@ -35,9 +36,11 @@ from dataclasses import replace
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+sys.path.insert(0, HERE)
 
 import torch  # noqa: E402
 
+from make_trajectory import fixture_name, schedule_config  # noqa: E402
 from oracle import attention as oattn  # noqa: E402
 from oracle import model as om  # noqa: E402
 
@@ -56,8 +59,9 @@ def linear_f64(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, dtype:
 
 def main() -> None:
     variation = sys.argv[1] if len(sys.argv) > 1 else "f64_linear"
+    schedule = sys.argv[2] if len(sys.argv) > 2 else "spike"
     torch.set_num_threads(8 if variation == "eight_threads" else THREADS)
-    config = om.baseline_config("A", steps=STEPS)
+    config = schedule_config(schedule)
     if variation == "f64_linear":
         om.linear = linear_f64
         note = "dense linears accumulate in float64 instead of float32"
@@ -85,14 +89,15 @@ def main() -> None:
         rows.append([rec["loss"], rec["learning_rate"], rec["grad_norm"]])
         print(f"step {i + 1}: {rows[-1]} ({time.time() - t0:.1f} s)", flush=True)
     out = {
-        "config": "A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup 2 cosine, 20 steps",
+        "config": (f"A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup "
+                   f"{config.optimizer.warmup_steps} cosine, 20 steps"),
         "perturbation": note,
         "seed": SEED,
         "windows": "numpy default_rng(0).integers(0, 50304, (20, 8, 1025), int32)",
         "columns": ["loss", "learning_rate", "grad_norm"],
         "rows": rows,
     }
-    with open(os.path.join(HERE, f"config_a_trajectory_{variation}.json"), "w") as f:
+    with open(os.path.join(HERE, fixture_name(schedule, variation)), "w") as f:
         json.dump(out, f, indent=1)
 
 

@@ -124,7 +124,7 @@ KEEP_CASES = [
     (2056, 256, 1300, 1297),
     (4096, 768, 5000, 4999),
     (8, 128, 600, 600),
-    (1536, 384, 2311, 2000),
+    (1536, 384, 2312, 2000),
 ]
 
 
@@ -159,6 +159,47 @@ def test_kept_softmax_pair_matches_oracle_and_forward(n, d, V, sv):
     # the order of those adds, one bf16 step at most.)
     assert maxabs(dh2, dhk) <= 1e-2 * sh
     assert maxabs(dw2 - base, dwk) <= 1e-5 * max(1.0, float(base.abs().max()))
+
+
+def test_kept_softmax_token_chunks_equal_one_chunk():
+    """The trainer's bounded form of the kept-softmax pair: the tokens cut into
+    chunks (of 1024 and a ragged 520), each chunk's forward and backward run
+    back to back with dW accumulated, against the oracle and against one call
+    over all tokens.  Losses and lse are per token, so they are bit-equal; dh
+    rows are per token too (equal up to the dh GEMM's split-K order); dW sums
+    the chunks in another order (f32)."""
+    from gptrig.kernels import linear_cross_entropy as lce
+
+    n, d, V, sv = 3592, 256, 3000, 2998
+    print(f"flce kept token chunks n={n} d={d} V={V}", flush=True)
+    h, w, t = inputs(n, d, V, sv, 81, 0.5, 0.5)
+    t[::13] = -1
+    losses_ref, lse_ref = oflce.losses_and_lse(h, w, t, semantic_vocab_size=sv, vocab_tile_size=256)
+    ct = torch.full((n,), 1.0 / n)
+    dh_ref, dw_ref = oflce.losses_backward(h, w, t, lse_ref, ct, semantic_vocab_size=sv, vocab_tile_size=256)
+    l1, ls1, dh1, dw1 = run_keep(h, w, t, sv, scale=1.0 / n)
+    hg, wg, tg = h.to(DEV), w.to(torch.bfloat16).to(DEV), t.to(DEV)
+    dw = torch.empty(V, d, device=DEV)
+    parts_l, parts_s, parts_dh = [], [], []
+    keep = None
+    for c0 in range(0, n, 1024):
+        c1 = min(n, c0 + 1024)
+        lc, lsc, keep = lce.flce_forward_keep(hg[c0:c1], wg, tg[c0:c1], sv, keep)
+        dhc, _ = lce.flce_backward_keep(hg[c0:c1], wg, tg[c0:c1], lsc, keep, None, 1.0 / n, sv, dweight=dw,
+                                        accumulate=c0 > 0)
+        parts_l.append(lc.cpu())
+        parts_s.append(lsc.cpu())
+        parts_dh.append(dhc.cpu())
+    torch.cuda.synchronize()
+    lk, lsk, dhk, dwk = torch.cat(parts_l), torch.cat(parts_s), torch.cat(parts_dh), dw.cpu()
+    fin = torch.isfinite(l1)
+    assert torch.equal(torch.isfinite(lk), fin) and torch.equal(lk[fin], l1[fin]) and torch.equal(lsk, ls1)
+    sh, sw = float(dh_ref.float().abs().max()), float(dw_ref.abs().max())
+    print(f"  dh {maxabs(dhk, dh_ref) / sh:.4f}, dW {maxabs(dwk, dw_ref) / sw:.4f} of max", flush=True)
+    assert maxabs(dhk, dh_ref) <= 2e-2 * sh and maxabs(dwk, dw_ref) <= 2e-2 * sw
+    assert maxabs(dhk, dh1) <= 1e-2 * sh
+    assert maxabs(dwk, dw1) <= 1e-3 * sw
+    assert (dwk[sv:] == 0).all()
 
 
 CHUNKED_CASES = [

@@ -509,9 +509,10 @@ def test_moe_routing_bit_exact():
     order = torch.empty(T * k, dtype=torch.int32, device=DEV)
     rows = torch.empty(T * k, dtype=torch.int32, device=DEV)
     position = torch.empty(T * k, dtype=torch.int32, device=DEV)
+    ws = _lib.workspace(_lib.query("gptrig_moe_route_workspace_bytes", T, E, k), lg.device)
     _lib.call("gptrig_moe_route", lg.data_ptr(), probs.data_ptr(), chosen.data_ptr(), gate.data_ptr(),
-              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), None, 0, T, E, k,
-              _lib.stream())
+              counts.data_ptr(), order.data_ptr(), rows.data_ptr(), position.data_ptr(), ws.data_ptr(), ws.numel(),
+              T, E, k, _lib.stream())
     torch.cuda.synchronize()
     assert torch.equal(chosen.cpu(), chosen_r)
     assert torch.equal(counts.cpu(), counts_r)
