@@ -54,6 +54,9 @@ def parse_args():
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention (B) and FLCE (C) configs")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the 4x32 micro-batch split and the config-E (MoE) step lines")
+    ap.add_argument("--config-e", action="store_true",
+                    help="run only the config-E (MoE) step lines, as one JSON object (the program profiled for the "
+                         "MoE kernel table)")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="run one 256 MiB calibration copy, one FLCE forward+backward and one attention "
                          "forward+backward at the bench's micro-batch shapes, and exit (the program profiled by "
@@ -420,6 +423,10 @@ def main():
     args = parse_args()
     if args.traffic_pass:
         traffic_pass(args.micro_batch)
+        return
+    if args.config_e:
+        print(json.dumps({"config_E_moe_step": {"reference_valid_width": moe_step(2, args.warmup, args.steps),
+                                                "baseline_width": moe_step(4, args.warmup, args.steps)}}), flush=True)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU (--gpus > 1) is not implemented",
