@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "gptrig")
 LIB = os.path.join(OUT_DIR, "libgptrig.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ("capi.hip", "elementwise.hip", "attention.hip", "flce.hip", "moe.hip", "linear.hip")
+SOURCES = ("capi.hip", "elementwise.hip", "attention.hip", "flce.hip", "flce32.hip", "moe.hip", "linear.hip")
 
 FLAGS = [
     "--offload-arch=gfx950",

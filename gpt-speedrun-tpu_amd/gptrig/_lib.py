@@ -34,6 +34,10 @@ SIGNATURES: dict[str, tuple] = {
     "gptrig_flce_fwd_noalloc": (I, [P, P, P, P, P, I, I, I, I, P]),
     "gptrig_flce_bwd_workspace_bytes": (Z, [I, I, I, I]),
     "gptrig_flce_bwd": (I, [P, P, P, P, P, F, P, P, I, P, Z, I, I, I, I, I, P]),
+    "gptrig_flce32_fwd_workspace_bytes": (Z, [I, I, I]),
+    "gptrig_flce32_fwd": (I, [P, P, P, P, P, P, Z, I, I, I, I, P]),
+    "gptrig_flce32_bwd_workspace_bytes": (Z, [I, I, I, I]),
+    "gptrig_flce32_bwd": (I, [P, P, P, P, P, F, P, P, I, P, Z, I, I, I, I, I, P]),
     "gptrig_flce_keep_bytes": (Z, [I, I]),
     "gptrig_flce_fwd_keep": (I, [P, P, P, P, P, P, Z, P, Z, I, I, I, I, P]),
     "gptrig_flce_bwd_keep_workspace_bytes": (Z, [I, I]),

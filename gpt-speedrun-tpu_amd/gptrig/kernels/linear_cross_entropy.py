@@ -7,10 +7,14 @@ ValueError/TypeError before any launch.  Neither direction materialises the
 at a time, and ``vocab_tile_size`` (rounded up to a multiple of 256, the
 kernels' tile) is that chunk: its bf16 softmax-gradient buffer is at most
 ``[tokens, chunk]``, the bound of the reference's ``[tokens, vocab_tile_size]``
-live logits (``:1-24``).  Matmul operands are bfloat16 (the reference's
-default ``compute_dtype``); logits, the online log-sum-exp, probabilities and
-accumulation are float32.  Any width is accepted: widths that are not a
-multiple of 64 are zero-padded, which leaves every logit unchanged.
+live logits (``:1-24``).  With ``compute_dtype=torch.bfloat16`` (the
+reference's default) the matmul operands are bfloat16; logits, the online
+log-sum-exp, probabilities and accumulation are float32.  Any width is
+accepted: widths that are not a multiple of 64 are zero-padded, which leaves
+every logit unchanged.  With ``compute_dtype=torch.float32`` every product and
+sum is float32 (``gptrig_flce32_*``: the same tiled algorithm on float32
+operands, a float32 ``[tokens, chunk]`` logit-gradient workspace); gradients
+come back in the inputs' dtypes, as the reference casts them (``:297-302``).
 """
 
 from __future__ import annotations
@@ -48,8 +52,8 @@ def _validate_inputs(hidden, embedding, targets, semantic_vocab_size: int, vocab
 def _normalize_compute_dtype(compute_dtype) -> torch.dtype:
     if not isinstance(compute_dtype, torch.dtype) or not compute_dtype.is_floating_point:
         raise TypeError(f"compute_dtype must be floating point, got {compute_dtype}")
-    if compute_dtype != torch.bfloat16:
-        raise TypeError(f"the HIP kernels compute in bfloat16; got compute_dtype={compute_dtype}")
+    if compute_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"the HIP kernels compute in bfloat16 or float32; got compute_dtype={compute_dtype}")
     return compute_dtype
 
 
@@ -223,13 +227,89 @@ class _TiledMean(torch.autograd.Function):
         return (*_unflatten(dh, dw, n, hshape, hdtype, edtype), None, None, None)
 
 
+def flce32_forward(h: torch.Tensor, w: torch.Tensor, t1: torch.Tensor, semantic_vocab_size: int):
+    """Per-token losses and LSE (f32 [n]) with float32 compute, for f32 ``h [n,d]``, ``w [V,d]``."""
+
+    n, d = h.shape
+    V = w.shape[0]
+    losses = torch.empty(n, dtype=torch.float32, device=h.device)
+    lse = torch.empty(n, dtype=torch.float32, device=h.device)
+    ws = _lib.workspace(_lib.query("gptrig_flce32_fwd_workspace_bytes", n, d, V), h.device)
+    _lib.call("gptrig_flce32_fwd", h.data_ptr(), w.data_ptr(), t1.data_ptr(), losses.data_ptr(), lse.data_ptr(),
+              ws.data_ptr(), ws.numel(), n, d, V, int(semantic_vocab_size), _lib.stream())
+    return losses, lse
+
+
+def flce32_backward(h, w, t1, lse, cotangent, cotangent_scale: float, semantic_vocab_size: int, vocab_chunk: int):
+    """``(dh f32 [n, d], dW f32 [V, d])`` with float32 compute."""
+
+    n, d = h.shape
+    V = w.shape[0]
+    dh = torch.empty((n, d), dtype=torch.float32, device=h.device)
+    dw = torch.empty((V, d), dtype=torch.float32, device=h.device)
+    ws = _lib.workspace(_lib.query("gptrig_flce32_bwd_workspace_bytes", n, d, V, int(vocab_chunk)), h.device)
+    _lib.call("gptrig_flce32_bwd", h.data_ptr(), w.data_ptr(), t1.data_ptr(), lse.data_ptr(), _lib.ptr(cotangent),
+              float(cotangent_scale), dh.data_ptr(), dw.data_ptr(), 0, ws.data_ptr(), ws.numel(), n, d, V,
+              int(semantic_vocab_size), int(vocab_chunk), _lib.stream())
+    return dh, dw
+
+
+def _flatten32(hidden, embedding, targets):
+    d = hidden.shape[-1]
+    return (hidden.reshape(-1, d).to(torch.float32).contiguous(), embedding.to(torch.float32).contiguous(),
+            targets.reshape(-1).to(torch.int32).contiguous())
+
+
+class _TiledLosses32(torch.autograd.Function):
+    """``tiled_tied_cross_entropy_losses`` with ``compute_dtype=float32``."""
+
+    @staticmethod
+    def forward(ctx, hidden, embedding, targets, semantic_vocab_size, chunk):
+        h, w, t1 = _flatten32(hidden, embedding, targets)
+        losses, lse = flce32_forward(h, w, t1, semantic_vocab_size)
+        ctx.save_for_backward(h, w, t1, lse)
+        ctx.cfg = (semantic_vocab_size, chunk, hidden.shape, hidden.dtype, embedding.dtype)
+        return losses.reshape(targets.shape)
+
+    @staticmethod
+    def backward(ctx, ct):
+        h, w, t1, lse = ctx.saved_tensors
+        sv, chunk, hshape, hdtype, edtype = ctx.cfg
+        cot = ct.reshape(-1).to(torch.float32).contiguous()
+        dh, dw = flce32_backward(h, w, t1, lse, cot, 0.0, sv, chunk)
+        return dh.reshape(hshape).to(hdtype), dw.to(edtype), None, None, None
+
+
+class _TiledMean32(torch.autograd.Function):
+    """``tiled_tied_cross_entropy`` with ``compute_dtype=float32``."""
+
+    @staticmethod
+    def forward(ctx, hidden, embedding, targets, semantic_vocab_size, chunk):
+        h, w, t1 = _flatten32(hidden, embedding, targets)
+        losses, lse = flce32_forward(h, w, t1, semantic_vocab_size)
+        ctx.save_for_backward(h, w, t1, lse)
+        ctx.cfg = (semantic_vocab_size, chunk, hidden.shape, hidden.dtype, embedding.dtype)
+        return losses.mean()
+
+    @staticmethod
+    def backward(ctx, ct):
+        h, w, t1, lse = ctx.saved_tensors
+        sv, chunk, hshape, hdtype, edtype = ctx.cfg
+        n = h.shape[0]
+        cot = (ct.to(torch.float32) / n).expand(n).contiguous()
+        dh, dw = flce32_backward(h, w, t1, lse, cot, 0.0, sv, chunk)
+        return dh.reshape(hshape).to(hdtype), dw.to(edtype), None, None, None
+
+
 def _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, compute_dtype):
     semantic_vocab_size = int(semantic_vocab_size)
     vocab_tile_size = int(vocab_tile_size)
-    _normalize_compute_dtype(compute_dtype)
+    dtype = _normalize_compute_dtype(compute_dtype)
     _validate_inputs(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size)
     _lib.require_device(hidden, embedding, targets)
-    return semantic_vocab_size, chunk_for(vocab_tile_size)
+    if dtype == torch.float32:
+        return semantic_vocab_size, int(vocab_tile_size), True
+    return semantic_vocab_size, chunk_for(vocab_tile_size), False
 
 
 def tiled_tied_cross_entropy_losses(hidden, embedding, targets, *, semantic_vocab_size: int,
@@ -238,8 +318,8 @@ def tiled_tied_cross_entropy_losses(hidden, embedding, targets, *, semantic_voca
     """One float32 cross-entropy value per target (``:308-346``); invalid
     targets give +inf and no gradient."""
 
-    sv, chunk = _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, compute_dtype)
-    return _TiledLosses.apply(hidden, embedding, targets, sv, chunk)
+    sv, chunk, f32 = _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, compute_dtype)
+    return (_TiledLosses32 if f32 else _TiledLosses).apply(hidden, embedding, targets, sv, chunk)
 
 
 def tiled_tied_cross_entropy(hidden, embedding, targets, *, semantic_vocab_size: int,
@@ -247,5 +327,5 @@ def tiled_tied_cross_entropy(hidden, embedding, targets, *, semantic_vocab_size:
                              compute_dtype=torch.bfloat16) -> torch.Tensor:
     """Mean tiled cross entropy in float32 (``:349-368``)."""
 
-    sv, chunk = _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, compute_dtype)
-    return _TiledMean.apply(hidden, embedding, targets, sv, chunk)
+    sv, chunk, f32 = _prepare(hidden, embedding, targets, semantic_vocab_size, vocab_tile_size, compute_dtype)
+    return (_TiledMean32 if f32 else _TiledMean).apply(hidden, embedding, targets, sv, chunk)

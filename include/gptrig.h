@@ -125,6 +125,24 @@ int gptrig_flce_bwd(const void* hidden, const void* weight, const int32_t* targe
                     int accumulate_dweight, void* workspace, size_t workspace_bytes, int n, int d, int vocab,
                     int semantic_vocab, int vocab_chunk, void* stream);
 
+/* The same forward and backward with float32 compute, the reference's
+ * compute_dtype=float32 (rig/kernels/linear_cross_entropy.py:38-41,
+ * _tile_logits :92-112): hidden f32 [n, d], weight f32 [vocab, d], every
+ * product and sum in float32 (lse and losses as gptrig_flce_fwd); the
+ * backward recomputes the logits per chunk of vocab_chunk rows (0: 2048,
+ * rounded up to 64) with a float32 [n, chunk] logit-gradient workspace, the
+ * reference's [n, vocab_tile_size] bound, and writes dhidden f32 [n, d] and
+ * dweight f32 [vocab, d] (+= with accumulate_dweight).  Any n, d. */
+size_t gptrig_flce32_fwd_workspace_bytes(int n, int d, int vocab);
+int gptrig_flce32_fwd(const float* hidden, const float* weight, const int32_t* targets, float* losses, float* lse,
+                      void* workspace, size_t workspace_bytes, int n, int d, int vocab, int semantic_vocab,
+                      void* stream);
+size_t gptrig_flce32_bwd_workspace_bytes(int n, int d, int vocab, int vocab_chunk);
+int gptrig_flce32_bwd(const float* hidden, const float* weight, const int32_t* targets, const float* lse,
+                      const float* cotangent, float cotangent_scale, float* dhidden, float* dweight,
+                      int accumulate_dweight, void* workspace, size_t workspace_bytes, int n, int d, int vocab,
+                      int semantic_vocab, int vocab_chunk, void* stream);
+
 /* Kept-softmax forward and backward: the one-chunk backward without the
  * logits recompute.  The reference's backward recomputes the logits tile by
  * tile from the saved (hidden, weight) (rig/kernels/linear_cross_entropy.py:

@@ -263,3 +263,79 @@ def test_width_five_bfloat16_fixture():
     assert maxabs(hg.grad, h2.grad) <= 2e-2 * float(h2.grad.float().abs().max())
     assert maxabs(eg.grad, e2.grad) <= 2e-2 * float(e2.grad.abs().max())
     assert (eg.grad[11:] == 0).all()
+
+
+def test_float32_compute_reference_fixture():
+    """compute_dtype=float32 (rig/kernels/linear_cross_entropy.py:38-41) on
+    the reference's own float32 cases (tests/test_linear_cross_entropy.py:
+    84-127): hidden (2, 3, 5) from default_rng(7), embedding (13, 5) from
+    default_rng(11), semantic vocabulary 11, tile 4; per-token losses within
+    rtol = atol = 2e-6 of the dense float32 oracle, the mean and both
+    gradients within 3e-6, storage-only rows' gradient exactly zero."""
+    from gptrig.kernels import tiled_tied_cross_entropy, tiled_tied_cross_entropy_losses
+
+    hidden = torch.from_numpy(np.random.default_rng(7).normal(size=(2, 3, 5)).astype(np.float32))
+    embedding = torch.from_numpy(np.random.default_rng(11).normal(size=(13, 5)).astype(np.float32))
+    targets = torch.tensor([[0, 1, 10], [3, 8, 6]], dtype=torch.int32)
+    print("flce float32 compute, reference fixture", flush=True)
+    losses = tiled_tied_cross_entropy_losses(hidden.to(DEV), embedding.to(DEV), targets.to(DEV),
+                                             semantic_vocab_size=11, vocab_tile_size=4, compute_dtype=torch.float32)
+    want = oflce.dense_losses(hidden, embedding, targets, 11, torch.float32)
+    np.testing.assert_allclose(losses.cpu().numpy(), want.numpy(), rtol=2e-6, atol=2e-6)
+    hg = hidden.to(DEV).requires_grad_(True)
+    eg = embedding.to(DEV).requires_grad_(True)
+    value = tiled_tied_cross_entropy(hg, eg, targets.to(DEV), semantic_vocab_size=11, vocab_tile_size=4,
+                                     compute_dtype=torch.float32)
+    value.backward()
+    h2 = hidden.clone().requires_grad_(True)
+    e2 = embedding.clone().requires_grad_(True)
+    dense = oflce.dense_losses(h2, e2, targets, 11, torch.float32).mean()
+    dense.backward()
+    print(f"  gpu {float(value):.8f} dense {float(dense):.8f}", flush=True)
+    assert abs(float(value) - float(dense)) <= 2e-6 + 2e-6 * abs(float(dense))
+    np.testing.assert_allclose(hg.grad.cpu().numpy(), h2.grad.numpy(), rtol=3e-6, atol=3e-6)
+    np.testing.assert_allclose(eg.grad.cpu().numpy(), e2.grad.numpy(), rtol=3e-6, atol=3e-6)
+    assert hg.grad.dtype == torch.float32 and eg.grad.dtype == torch.float32
+    assert (eg.grad[11:] == 0).all()
+
+
+@pytest.mark.parametrize("n,d,V,sv,tile", [(300, 96, 1000, 997, 256), (1030, 200, 3001, 2900, 2048), (8, 5, 13, 11, 4)])
+def test_float32_compute_matches_float64_dense(n, d, V, sv, tile):
+    """The float32 path against the float64 dense closed form at larger,
+    ragged shapes (tokens, width, vocabulary and chunks not multiples of the
+    64 tile), with invalid targets (+inf loss, no gradient) and per-token
+    cotangents: losses to 2e-6 relative, gradients to 1e-5 of their scale."""
+    from gptrig.kernels import tiled_tied_cross_entropy_losses
+
+    g = torch.Generator().manual_seed(91)
+    h = torch.randn((n, d), generator=g)
+    w = torch.randn((V, d), generator=g) * 0.3
+    t = torch.randint(0, sv, (n,), generator=g, dtype=torch.int32)
+    t[::17] = -1
+    ct = torch.rand(n, generator=g)
+    print(f"flce float32 compute n={n} d={d} V={V} sv={sv} tile={tile}", flush=True)
+    hg = h.to(DEV).requires_grad_(True)
+    wg = w.to(DEV).requires_grad_(True)
+    losses = tiled_tied_cross_entropy_losses(hg, wg, t.to(DEV), semantic_vocab_size=sv, vocab_tile_size=tile,
+                                             compute_dtype=torch.float32)
+    finite = torch.isfinite(losses)
+    (losses[finite] * ct.to(DEV)[finite]).sum().backward()
+    h64 = h.double().requires_grad_(True)
+    w64 = w.double().requires_grad_(True)
+    logits = h64 @ w64[:sv].t()
+    valid = t >= 0
+    lse = torch.logsumexp(logits, -1)
+    ref = torch.full((n,), float("inf"), dtype=torch.float64)
+    ref[valid] = lse[valid] - logits[valid].gather(1, t[valid].long()[:, None])[:, 0]
+    (ref[valid] * ct.double()[valid]).sum().backward()
+    lc = losses.detach().cpu().double()
+    assert torch.equal(torch.isfinite(lc), valid)
+    rel = ((lc[valid] - ref[valid]).abs() / ref[valid].abs()).max()
+    print(f"  loss rel {float(rel):.2e}", flush=True)
+    assert float(rel) <= 2e-6
+    for got, want in ((hg.grad, h64.grad), (wg.grad, w64.grad)):
+        err = float((got.cpu().double() - want).abs().max())
+        scale = float(want.abs().max())
+        print(f"  grad max-abs {err:.3e} of {scale:.3e}", flush=True)
+        assert err <= 1e-5 * scale
+    assert (wg.grad[sv:] == 0).all()
