@@ -11,11 +11,13 @@ float32 summation order, and this trajectory is chaotic enough around its
 loss spike (steps 4-9) that the same code on 8 threads differs by about 0.5%
 at step 8 (``make_trajectory_perturbed.py eight_threads``).
 
-A second schedule, ``long_warmup``, warms the learning rate up over all 20
-steps (2^-8 reached at step 20) instead of 2: its run has no loss spike, and
-the reference-equivalent variations of ``make_trajectory_perturbed.py`` stay
-within 0.1% of it at every step, so a GPU run can be held to 1% of this
-fixture alone.
+A second schedule, ``long_warmup``, is the first 20 steps of a 40-step run
+whose learning rate warms up over all 40 (so 2^-8 x step / 40, at most 2^-9):
+its run has no loss spike, and the reference-equivalent variations of
+``make_trajectory_perturbed.py`` stay within 0.1% of it at every step, so a
+GPU run can be held to 1% of this fixture alone.  (Warming up over the 20
+steps themselves is not enough: the runs part by up to 0.6% over the last
+three steps, where the rate nears 2^-8.)
 
 Usage: ``python tests/golden/make_trajectory.py [long_warmup]`` (about 12
 minutes).  Output: ``tests/golden/config_a_trajectory.json`` (or
@@ -42,16 +44,18 @@ SEED = 0
 THREADS = 3
 
 
-SCHEDULES = {"spike": None, "long_warmup": STEPS}  # warmup steps (None: the config's 10%)
+# (schedule length, warmup steps); the fixtures hold the first STEPS steps.
+SCHEDULES = {"spike": (STEPS, None), "long_warmup": (2 * STEPS, 2 * STEPS)}
 
 
 def schedule_config(schedule: str):
-    """Config A with the named learning-rate warmup."""
+    """Config A with the named learning-rate schedule (``None``: the config's
+    10% warmup)."""
 
     from dataclasses import replace
 
-    config = om.baseline_config("A", steps=STEPS)
-    warmup = SCHEDULES[schedule]
+    length, warmup = SCHEDULES[schedule]
+    config = om.baseline_config("A", steps=length)
     if warmup is not None:
         config = replace(config, optimizer=replace(config.optimizer, warmup_steps=warmup))
     return config
@@ -77,7 +81,7 @@ def main() -> None:
         print(f"step {i + 1}: {rows[-1]} ({time.time() - t0:.1f} s)", flush=True)
     out = {
         "config": (f"A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup "
-                   f"{config.optimizer.warmup_steps} cosine, 20 steps"),
+                   f"{config.optimizer.warmup_steps} of {config.optimizer.steps} steps, cosine, first {STEPS} steps"),
         "seed": SEED,
         "windows": "numpy default_rng(0).integers(0, 50304, (20, 8, 1025), int32)",
         "columns": ["loss", "learning_rate", "grad_norm"],

@@ -90,7 +90,7 @@ def main() -> None:
         print(f"step {i + 1}: {rows[-1]} ({time.time() - t0:.1f} s)", flush=True)
     out = {
         "config": (f"A: 8L d512 8x64 vocab 50304 seq 1024 batch 8, AdamW lr 2^-8 warmup "
-                   f"{config.optimizer.warmup_steps} cosine, 20 steps"),
+                   f"{config.optimizer.warmup_steps} of {config.optimizer.steps} steps, cosine, first {STEPS} steps"),
         "perturbation": note,
         "seed": SEED,
         "windows": "numpy default_rng(0).integers(0, 50304, (20, 8, 1025), int32)",

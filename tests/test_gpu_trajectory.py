@@ -24,6 +24,16 @@ loss trajectory within 1%" against that set:
     against the closest run.  The gradient norm is the noisier figure (Adam
     turns last-bit gradient differences into parameter differences): the
     equivalent runs differ from one another by up to 57% on single steps.
+The equivalent runs are the 8-thread, float64-linear and dense-attention
+restatements; the kernel's test-oracle attention (normalised probabilities
+rounded before the PV product) is not the forward the reference's training
+step runs, so it is not one of them.  The test prints which run was closest.
+
+A second gate holds the GPU to one fixture alone, on a schedule with no loss
+spike: the first 20 steps of a 40-step run whose learning rate warms up over
+all 40 (``config_a_long_warmup_trajectory.json``).  There the three
+restatements stay within 0.033% of the fixture at every step, so every GPU
+step must be within 1% of the fixture itself.
 """
 
 from __future__ import annotations
@@ -41,30 +51,39 @@ pytestmark = pytest.mark.gpu
 
 FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "config_a_trajectory.json")
 # The oracle's runs that the reference treats as the same computation.
-EQUIVALENT_RUNS = ("eight_threads", "f64_linear", "normalized_attention", "dense_attention")
+EQUIVALENT_RUNS = ("eight_threads", "f64_linear", "dense_attention")
+LONG_WARMUP_FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "config_a_long_warmup_trajectory.json")
 
 
-def test_config_a_twenty_step_trajectory_matches_oracle():
+def run_config_a(steps: int, schedule_steps: int, warmup_steps):
+    """The GPU trainer's first ``steps`` steps of config A (seed-0 parameters
+    and token windows, as the fixtures) on a ``schedule_steps``-step schedule
+    (``warmup_steps`` None: the config's 10%); returns its history rows."""
     from gptrig.optim import OptimizerConfig
     from gptrig.train import GPTConfig, GPTTrainer
 
-    with open(FIXTURE) as f:
-        want = np.asarray(json.load(f)["rows"], dtype=np.float64)
-    steps = want.shape[0]
-    ocfg = om.baseline_config("A", steps=steps)
+    ocfg = om.baseline_config("A", steps=schedule_steps)
+    warmup = ocfg.optimizer.warmup_steps if warmup_steps is None else warmup_steps
     cfg = GPTConfig(layers=ocfg.layers, heads=ocfg.heads, d_model=ocfg.d_model, vocab_size=ocfg.vocab_size,
                     semantic_vocab_size=ocfg.semantic_vocab_size, seq_len=ocfg.seq_len,
                     batch_size=ocfg.batch_size, micro_batch_size=ocfg.batch_size, base_width=ocfg.base_width,
                     base_depth=ocfg.base_depth, attention_scale=ocfg.attention_scale, embeddings=ocfg.embeddings,
-                    optimizer=OptimizerConfig(learning_rate=ocfg.optimizer.learning_rate, steps=steps,
-                                              warmup_steps=ocfg.optimizer.warmup_steps))
+                    optimizer=OptimizerConfig(learning_rate=ocfg.optimizer.learning_rate, steps=schedule_steps,
+                                              warmup_steps=warmup))
     windows = torch.from_numpy(om.synthetic_windows(0, steps, cfg.batch_size, cfg.seq_len, cfg.vocab_size))
-    print(f"trajectory case config A, {steps} steps", flush=True)
+    print(f"trajectory case config A, {steps} steps of a {schedule_steps}-step schedule, warmup {warmup}", flush=True)
     trainer = GPTTrainer(cfg, seed=0)
     dev_windows = windows.cuda()
     for i in range(steps):
         trainer.train_step(dev_windows[i, :, :-1], dev_windows[i, :, 1:])
-    got = trainer.history_rows()
+    return trainer.history_rows()
+
+
+def test_config_a_twenty_step_trajectory_matches_oracle():
+    with open(FIXTURE) as f:
+        want = np.asarray(json.load(f)["rows"], dtype=np.float64)
+    steps = want.shape[0]
+    got = run_config_a(steps, steps, None)
     golden = os.path.dirname(FIXTURE)
     runs = {"fixture": want}
     for variation in EQUIVALENT_RUNS:
@@ -91,3 +110,20 @@ def test_config_a_twenty_step_trajectory_matches_oracle():
     assert np.all(rel[:3] <= 1e-2), rel[:3]
     rel_near = np.abs(got[:, 2] - near[:, 2]) / near[:, 2]
     assert float(np.median(rel_near)) <= 5e-2, rel_near
+
+
+def test_config_a_long_warmup_trajectory_within_one_percent_of_the_fixture():
+    with open(LONG_WARMUP_FIXTURE) as f:
+        want = np.asarray(json.load(f)["rows"], dtype=np.float64)
+    steps = want.shape[0]
+    got = run_config_a(steps, 2 * steps, 2 * steps)
+    loss_rel = np.abs(got[:, 0] - want[:, 0]) / want[:, 0]
+    print("gpu losses   ", np.round(got[:, 0], 4).tolist(), flush=True)
+    print("oracle losses", np.round(want[:, 0], 4).tolist(), flush=True)
+    print("loss relative differences", np.round(loss_rel, 5).tolist(), flush=True)
+    assert float(loss_rel.max()) <= 1e-2, loss_rel
+    np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-6)
+    rel = np.abs(got[:, 2] - want[:, 2]) / want[:, 2]
+    print("grad norm relative differences", np.round(rel, 4).tolist(), flush=True)
+    assert np.all(rel[:3] <= 1e-2), rel[:3]
+    assert float(np.median(rel)) <= 5e-2, rel
