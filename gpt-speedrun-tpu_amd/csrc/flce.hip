@@ -17,9 +17,15 @@
 //            K2  dW[chunk] += G^T h;
 //            K3  dh       += G W[chunk], rounded to bf16 after the last chunk.
 //            One chunk (the whole vocabulary): three launches, K2 and K3 split
-//            over their reduction with fp32 atomics.  Several chunks: one
-//            persistent work-queue launch (flce_bwd_queue_kernel) that
-//            pipelines K1 / K2 / K3 of successive chunks.
+//            over their reduction with fp32 atomics.  Several chunks:
+//            nchunks + 1 pipelined launches of flce_bwd_pipe_kernel over two
+//            halves of the G^T buffer -- launch c runs K2 / K3 of chunk c - 1
+//            from one half and K1 of chunk c into the other, its workgroups
+//            taking items from per-XCD token-block counters and never
+//            waiting for one another (the stream orders the launches).
+//   kept-softmax forward / backward: the forward also stores fp16
+//            exp(logit - max) in the blocked G^T layout; the backward
+//            rescales it in place to G instead of recomputing the logits.
 #include "gemm_core.h"
 
 #include <math.h>
@@ -64,9 +70,15 @@ __device__ __forceinline__ float2 column_stats(f32x16 (&acc)[4][2], int nb, int 
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+
 // column_stats that also stores every fp16 exp2(logit * log2(e) - max) of the
-// column (this wave's 128 vocabulary rows x one token) at col + 32 * row, for
-// the rows below vlim (the storage vocabulary): the kept-softmax forward.
+// column (this wave's 128 vocabulary rows x one token), for the rows below
+// vlim (the storage vocabulary), in the kept layout: rows in groups of 4, a
+// group of 32 tokens as 256 contiguous bytes, token-major (element (v, n) at
+// ((n / 32) * (Vp / 4) + v / 4) * 128 + (n % 32) * 4 + v % 4, Vp = V rounded
+// up to 4).  The lane's 4 consecutive accumulator rows are one 8-byte store;
+// col points at its token's slot of the group holding row 0 of its block.
 // Nothing is stored for a column with no real row.
 template <bool kMask>
 __device__ __forceinline__ float2 column_stats_keep(f32x16 (&acc)[4][2], int nb, int lim, int vlim, f16* col) {
@@ -85,11 +97,23 @@ __device__ __forceinline__ float2 column_stats_keep(f32x16 (&acc)[4][2], int nb,
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(acc[mb][nb][i] - mx);
-        sum += p;
-        const int r = 32 * mb + 8 * (i >> 2) + (i & 3);
-        if (!kMask || r < vlim) col[32 * r] = (f16)p;
+      for (int q = 0; q < 4; ++q) {
+        f16x4 p4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float p = fast_exp2(acc[mb][nb][4 * q + t] - mx);
+          sum += p;
+          p4[t] = (f16)p;
+        }
+        const int r0 = 32 * mb + 8 * q;  // rows r0 .. r0 + 3 of the lane's block
+        f16* dst = col + (r0 / 4) * 128;
+        if (!kMask || r0 + 3 < vlim) {
+          *reinterpret_cast<f16x4*>(dst) = p4;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (r0 + t < vlim) dst[t] = p4[t];
+        }
       }
   }
   sum += __shfl_xor(sum, 32);
@@ -136,10 +160,9 @@ __global__ void __launch_bounds__(gemm::THREADS)
 // LDS-only barriers (a full __syncthreads would wait for those copies).
 // kKeep (the kept-softmax forward): every probability exp2(y - m) of the
 // tile, m the max over its wave's 128 vocabulary rows, is also stored as fp16
-// in the blocked G^T layout of the one-chunk backward (element (v, n) at
-// ((n / 32) * V + v) * 32 + n % 32, v < V), and m at
-// mhalf[(2 tile + half) * N + n], so the backward rescales them instead of
-// recomputing the logits.
+// in the kept layout of column_stats_keep, and m at
+// mhalf[(2 tile + half) * N + n], so the backward rescales them (in place,
+// into the blocked G^T layout) instead of recomputing the logits.
 template <bool kKeep>
 __global__ void __launch_bounds__(gemm::THREADS)
     flce_fwd_persistent_kernel(Operand W, Operand Hd, int V, int N, int D, int sem_v, float2* __restrict__ partial,
@@ -160,8 +183,9 @@ __global__ void __launch_bounds__(gemm::THREADS)
       const int n = tn * BN + 64 * wn + 32 * nb + l32;
       float2 st;
       if constexpr (kKeep) {
-        // Tokens past n are not stored: their column points at row 0.
-        f16* col = keep + (n < N ? ((size_t)(n >> 5) * V + vbase + 4 * hl) * 32 + (n & 31) : 0);
+        // Tokens past N are not stored: their column points at row 0.
+        const int vq = (V + 3) / 4;  // row groups per 32-token block
+        f16* col = keep + (n < N ? ((size_t)(n >> 5) * vq + (vbase + 4 * hl) / 4) * 128 + (n & 31) * 4 : 0);
         const int vlim = V - vbase - 4 * hl;
         if (n < N)
           st = full ? column_stats_keep<false>(acc, nb, lim, vlim, col)
@@ -799,7 +823,11 @@ int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targe
 // blocks of [vocab][32]; fp16 probabilities from the forward, rewritten in
 // place as the bf16 gradient), then the f32 per-(half tile, token) maxima
 // [2 ceil(vocab/256)][n].
-size_t keep_gt_bytes(int n, int vocab) { return align256((size_t)vocab * ceil_div(n, 32) * 32 * sizeof(bf16)); }
+// Rows of the kept / G^T blocks: the vocabulary rounded up to a group of 4.
+int keep_rows(int vocab) { return (vocab + 3) / 4 * 4; }
+size_t keep_gt_bytes(int n, int vocab) {
+  return align256((size_t)keep_rows(vocab) * ceil_div(n, 32) * 32 * sizeof(bf16));
+}
 
 // Backward from the kept softmax, step 1: the per-(half tile, token) maxima m
 // become the factors a = exp2(m - lse log2(e)) ct of their probabilities (in
@@ -825,36 +853,40 @@ __global__ void flce_keep_alpha_kernel(float* __restrict__ mh, int halves, int N
 
 // Step 2: G^T[v][n] = bf16(p a - [v == t] ct), zero for v >= semantic vocab
 // (K1's values, from the kept fp16 p instead of recomputed logits), in place:
-// blockIdx.y = the 32-token block, one thread per 8 tokens of one row,
-// consecutive threads on consecutive 16 bytes.
+// each 256-byte group (4 rows x 32 tokens, token-major) becomes the same 256
+// bytes of the blocked G^T layout (element (v, n) at ((n / 32) Vp + v) 32 +
+// n % 32).  16 consecutive lanes take one group, 16 bytes (2 tokens x 4 rows)
+// each, and all of a group's loads precede its stores (one wave, one load
+// instruction), so the in-place transpose never reads a rewritten byte.
 __global__ void __launch_bounds__(256)
     flce_keep_rescale_kernel(bf16* __restrict__ gt, const float* __restrict__ alpha, int N, int V, int sem_v,
                              const int32_t* __restrict__ targets, const float* __restrict__ cot, float cot_scale) {
-  const int rem = blockIdx.x * 256 + threadIdx.x;
-  if (rem >= V * 4) return;
-  const int blk = blockIdx.y;
-  const int v = rem >> 2, c = rem & 3;
-  const int n0 = 32 * blk + 8 * c;
-  if (n0 >= N) return;  // N % 8 == 0: a group is wholly in or out
-  bf16* g = gt + ((size_t)blk * V + v) * 32 + 8 * c;
-  bf16x8 o = bf16x8{};
-  if (v < sem_v) {
-    const f16x8 p = *reinterpret_cast<const f16x8*>(g);
-    const float* a = alpha + (size_t)(2 * (v >> 8) + ((v >> 7) & 1)) * N + n0;
-    const f32x4 a0 = *reinterpret_cast<const f32x4*>(a);
-    const f32x4 a1 = *reinterpret_cast<const f32x4*>(a + 4);
-    const i32x4_t t0 = *reinterpret_cast<const i32x4_t*>(targets + n0);
-    const i32x4_t t1 = *reinterpret_cast<const i32x4_t*>(targets + n0 + 4);
+  const int vq = (V + 3) / 4;
+  const int gid = blockIdx.x * 16 + (threadIdx.x >> 4);  // row group of this 32-token block
+  if (gid >= vq) return;  // whole 16-lane groups leave together
+  const int blk = blockIdx.y, j = threadIdx.x & 15;
+  const int n = 32 * blk + 2 * j;
+  const int v0 = 4 * gid;
+  bf16* grp = gt + ((size_t)blk * vq + gid) * 128;
+  const f16x8 p = *reinterpret_cast<const f16x8*>(grp + 8 * j);  // tokens n, n + 1 x rows v0 .. v0 + 3
+  if (n >= N) return;  // N % 8 == 0: both tokens are in or out
+  bf16x2 o[4] = {};
+  if (v0 < sem_v) {
+    const float2 a = *reinterpret_cast<const float2*>(alpha + (size_t)(2 * (v0 >> 8) + ((v0 >> 7) & 1)) * N + n);
+    const int2 t = *reinterpret_cast<const int2*>(targets + n);
+    const float c0 = cot ? cot[n] : cot_scale, c1 = cot ? cot[n + 1] : cot_scale;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float aj = j < 4 ? a0[j] : a1[j - 4];
-      const int tj = j < 4 ? t0[j] : t1[j - 4];
-      float g8 = (float)p[j] * aj;
-      if (tj == v) g8 -= cot ? cot[n0 + j] : cot_scale;  // tj == v < sem_v: a valid target
-      o[j] = (bf16)g8;
+    for (int r = 0; r < 4; ++r) {
+      const int v = v0 + r;
+      if (v >= sem_v) continue;
+      float g0 = (float)p[r] * a.x, g1 = (float)p[4 + r] * a.y;
+      if (t.x == v) g0 -= c0;  // t == v < sem_v: a valid target
+      if (t.y == v) g1 -= c1;
+      o[r] = bf16x2{(bf16)g0, (bf16)g1};
     }
   }
-  *reinterpret_cast<bf16x8*>(g) = o;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) *reinterpret_cast<bf16x2*>(grp + r * 32 + 2 * j) = o[r];
 }
 
 }  // namespace
@@ -1145,16 +1177,16 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
   flce_keep_alpha_kernel<<<dim3((unsigned)ceil_div(n / 4, 256), (unsigned)halves), 256, 0, s>>>(
       alpha, halves, n, semantic_vocab, targets, lse, cotangent, cotangent_scale);
   GPTRIG_CHECK_LAUNCH();
-  const dim3 rgrid((unsigned)ceil_div(vocab * 4, 256), (unsigned)ceil_div(n, 32));
+  const dim3 rgrid((unsigned)ceil_div(keep_rows(vocab) / 4, 16), (unsigned)ceil_div(n, 32));
   flce_keep_rescale_kernel<<<rgrid, 256, 0, s>>>(gt, alpha, n, vocab, semantic_vocab, targets, cotangent,
                                                   cotangent_scale);
   GPTRIG_CHECK_LAUNCH();
   // dW (+)= G^T h and dh += G W.
-  Operand Ag{gt, n, vc}, Bh{Hp, d};
+  Operand Ag{gt, n, keep_rows(vocab)}, Bh{Hp, d};
   gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(Ag, Bh, vc, d, n, dw_split,
                                                                                       dweight, d, dw_mode, nullptr);
   GPTRIG_CHECK_LAUNCH();
-  Operand Agt{gt, n, vc}, Bw{Wp, d};
+  Operand Agt{gt, n, keep_rows(vocab)}, Bw{Wp, d};
   const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
   gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
                                                                                       dh_acc, d, 2, nullptr);
