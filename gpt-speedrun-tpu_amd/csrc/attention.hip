@@ -13,15 +13,12 @@
 // row max/sum are lane-local (+ one xor-32 exchange) and P^T is already the
 // B operand of O^T = V^T P^T, so probabilities never leave registers.
 //
-// Backward, head_dim 64: two kernels and no atomics, like the reference's
-// separate passes.  dQ is query-owned (the forward's mapping: S^T and dP^T
-// per wave, dQ^T = K^T dS^T from registers; it also forms Delta); dK / dV is
-// key-owned (128 keys per workgroup, S and dP with lane l holding key l%32,
-// dV^T += dO^T P and dK^T += Q^T dS in registers).
-// Backward, head_dim 128 (the older design): a workgroup owns 128 keys and
-// walks the causal query blocks (64 queries per step), publishes bf16 dS to
-// LDS, forms dQ = dS K over its 128 keys and adds it to an fp32 accumulator
-// with atomics; a last pass rounds dQ to bf16.
+// Backward mapping: a workgroup owns 128 keys (4 waves x 32) and walks the
+// causal query blocks (64 queries per step).  Each wave computes S = Q K^T and
+// dP = dO V^T with lane l holding key l%32, accumulates dV^T += dO^T P and
+// dK^T += Q^T dS in registers, and publishes bf16 dS to LDS; the workgroup
+// then forms dQ = dS K (all 128 keys) and adds it to an fp32 accumulator with
+// atomics.  A last pass rounds dQ to bf16.
 #include "attn64.h"
 
 #include <type_traits>
@@ -31,6 +28,8 @@ namespace {
 constexpr int kBlockM = 128;  // forward: queries per workgroup
 constexpr int kBlockN = 64;   // forward: keys per LDS tile
 constexpr int kBwdN = 128;    // backward (head_dim 128): keys per workgroup
+constexpr int kBwd64Threads = 512;  // backward (head_dim 64): 8 waves of 32 keys
+constexpr int kBwd64Keys = 256;     // backward (head_dim 64): keys per workgroup
 constexpr int kBwdM = 64;     // backward: queries per step
 constexpr float kMinusBig = -1.0e30f;
 
@@ -724,217 +723,71 @@ __global__ void __launch_bounds__(256, 4)
   }
 }
 
-// ---------------------------------------------------------------------------
-// head_dim 64 backward as two kernels with no atomics, like the reference's
-// separate dQ and dK/dV passes (tpu_flash_attention.py:479-575, :578-701).
-// ---------------------------------------------------------------------------
-
-// dQ (query-owned, the forward's mapping): a workgroup owns 128 queries (4
-// waves x 32); K / V tiles of 64 keys stream through the double-buffered
-// swizzled LDS tiles of the forward.  Each wave computes S^T = K Q^T and
-// dP^T = V dO^T, so MFMA lane l holds query l % 32 and lse / Delta are
-// per-lane scalars; dS^T is already the B operand of dQ^T = K^T dS^T (K^T
-// from transposed reads in the accumulator's row order), so nothing is
-// written to LDS but the tiles.  Delta = rowsum(O * dO) is formed here from
-// the lane's own O / dO values; lse * log2(e) and Delta * scale are stored
-// for the dK / dV kernel.  The dQ
-// epilogue applies the optional RoPE VJP (rcs / rsn: tables [S][D/2]).
+// Backward: KV-owned, 256 keys per workgroup (32 per wave), 64 queries per
+// step.  Q/dO/K/V tiles are swizzled row-major; Q^T, dO^T, K^T and dS come
+// from transposed reads, so nothing is written to LDS transposed.  dS is
+// stored as dS^T [key][query] (8-byte writes) and dQ = dS K is added to an
+// fp32 accumulator with buffer atomics.  The loop body keeps no spills: a
+// scratch reload would make the compiler wait for every outstanding vector
+// memory operation, the previous step's dQ atomics included.
 template <bool kSeg>
-__global__ void __launch_bounds__(256, 3)
-    attn_dq64_kernel(View Q, View K, View V, View O, View dO, const float* __restrict__ lse,
-                     const int32_t* __restrict__ seg, float* __restrict__ lse2_out, float* __restrict__ dsc_out,
-                     MutView dQ, int B, int H, int S,
-                     float scale, float scale_log2, const bf16* __restrict__ rcs, const bf16* __restrict__ rsn) {
-  constexpr int D = 64, KC = 4, DB = 2;
-  const int nq = (S + kBlockM - 1) / kBlockM;
-  int bh, qb;
-  xcd_map(blockIdx.x, nq, B * H, bh, qb);
-  qb = nq - 1 - qb;  // heaviest blocks first
-  const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hl = lane >> 5, l32 = lane & 31;
-  const int q0 = qb * kBlockM;
-  const int qw0 = q0 + wave * 32;
-  const int my_q = qw0 + l32;
-  const bool q_ok = my_q < S;
-  const int last_q = min(q0 + kBlockM, S) - 1;
-  const int ntiles = last_q / kBlockN + 1;
-
-  bf16x8 qreg[KC], greg[KC];
-  float delta = 0.f;
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    const int d0 = 16 * kc + 8 * hl;
-    qreg[kc] = q_ok ? *reinterpret_cast<const bf16x8*>(Q.row(b, h, my_q) + d0) : bf16x8{};
-    greg[kc] = q_ok ? *reinterpret_cast<const bf16x8*>(dO.row(b, h, my_q) + d0) : bf16x8{};
-    const bf16x8 ov = q_ok ? *reinterpret_cast<const bf16x8*>(O.row(b, h, my_q) + d0) : bf16x8{};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) delta += (float)ov[j] * (float)greg[kc][j];
-  }
-  delta += __shfl_xor(delta, 32);
-  const size_t row = (size_t)bh * S + my_q;
-  const float lse2 = q_ok ? lse[row] * GPTRIG_LOG2E : 0.f;
-  const float dsc = delta * scale;  // dS = P * (scale*dP - scale*Delta)
-  if (q_ok && hl == 0) {
-    lse2_out[row] = lse2;
-    dsc_out[row] = dsc;
-  }
-  const int seg_q = (kSeg && q_ok) ? seg[(size_t)b * S + my_q] : 0;
-
-  f32x16 acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
-
-  const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(K.row(b, h, 0), (uint32_t)(S * K.ss * 2));
-  const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(V.row(b, h, 0), (uint32_t)(S * V.ss * 2));
-  const int kss2 = (int)K.ss * 2, vss2 = (int)V.ss * 2;
-  int koff[2], voff[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 8 * (2 * wave + j) + (lane >> 3);
-    const int t = (r >> 1) & 7;
-    const int c = (lane & 7) ^ (((t & 1) << 2) | (t >> 1));
-    koff[j] = r * kss2 + 16 * c;
-    voff[j] = r * vss2 + 16 * c;
-  }
-  auto fill = [&](at64::lds_t* kt, at64::lds_t* vt, int kv0) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int blk = 2 * wave + j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, (lds_void*)(kt + blk * 512), 16, koff[j] + kv0 * kss2, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rs, (lds_void*)(vt + blk * 512), 16, voff[j] + kv0 * vss2, 0, 0, 0);
-    }
-  };
-
-  // One 32-key half of a tile: element i of the score accumulators holds key
-  // kh0 + 8 (i / 4) + 4 hl + i % 4 of query my_q.  kMask: the causal / ragged
-  // / segment mask per element (diagonal and edge halves only); the interior
-  // halves run a mask-free copy.
-  auto half = [&](const at64::lds_t* kt, const at64::lds_t* vt, int kv0, int sb, auto mask_tag)
-                  __attribute__((always_inline)) {
-    constexpr bool kMask = decltype(mask_tag)::value;
-    // (A fence first in the masked copy only: identical leading instructions
-    // would be hoisted above the branch between the copies.)
-    if constexpr (kMask) __builtin_amdgcn_sched_barrier(0);
-    f32x16 sacc = f32x16{}, pacc = f32x16{};
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      sacc = mfma32(at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl), qreg[kc], sacc);
-      pacc = mfma32(at64::rowfrag(vt, 32 * sb + l32, 2 * kc + hl), greg[kc], pacc);
-    }
-    const int kh0 = kv0 + 32 * sb;
-    const int lim = min(my_q, S - 1) - kh0 - 4 * hl;
-    bf16x8 dsb[2];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float p = fast_exp2(fmaf(sacc[i], scale_log2, -lse2));
-      if constexpr (kMask) {
-        const int c = 8 * (i >> 2) + (i & 3);
-        bool vis = c <= lim;
-        if (kSeg && vis) vis = seg[(size_t)b * S + kh0 + 4 * hl + c] == seg_q;
-        p = vis ? p : 0.f;
-      }
-      dsb[i >> 3][i & 7] = (bf16)(p * fmaf(pacc[i], scale, -dsc));
-    }
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        acc[db] = mfma32(at64::trfrag<true>(kt, 32 * db, 16 * (2 * sb + c2), lane), dsb[c2], acc[db]);
-  };
-  auto half_any = [&](const at64::lds_t* kt, const at64::lds_t* vt, int kv0, int sb) __attribute__((always_inline)) {
-    const int kh0 = kv0 + 32 * sb;
-    if (kSeg || (kh0 + 31 > qw0) || (kh0 + 32 > S))
-      half(kt, vt, kv0, sb, std::true_type{});
-    else
-      half(kt, vt, kv0, sb, std::false_type{});
-  };
-
-  auto tile = [&](const at64::lds_t* kt, const at64::lds_t* vt, at64::lds_t* nkt, at64::lds_t* nvt, int it) {
-    const int kv0 = it * kBlockN;
-    if (it + 1 < ntiles) fill(nkt, nvt, kv0 + kBlockN);
-    if (kv0 <= qw0 + 31) half_any(kt, vt, kv0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (kv0 + 32 <= qw0 + 31) half_any(kt, vt, kv0, 1);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
-    __syncthreads();
-  };
-
-  fill(fwd_k<0>(), fwd_v<0>(), 0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
-  for (int it = 0; it < ntiles; it += 2) {
-    tile(fwd_k<0>(), fwd_v<0>(), fwd_k<1>(), fwd_v<1>(), it);
-    if (it + 1 < ntiles) tile(fwd_k<1>(), fwd_v<1>(), fwd_k<0>(), fwd_v<0>(), it + 1);
-  }
-
-  if (q_ok) {
-    bf16* qrow = dQ.row(b, h, my_q);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bf16x4 o4;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) o4[t] = (bf16)acc[db][4 * r + t];
-        if (rcs) {  // RoPE VJP: d = 32db + 8r + 4hl + t, pairs (t, t+1) for t = 0, 2
-          const int j0 = (32 * db + 8 * r + 4 * hl) / 2;
-          const bf16x2 c2 = *reinterpret_cast<const bf16x2*>(rcs + (size_t)my_q * (D / 2) + j0);
-          const bf16x2 s2 = *reinterpret_cast<const bf16x2*>(rsn + (size_t)my_q * (D / 2) + j0);
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const bf16x2 rr = rope_pair((float)o4[2 * u], (float)o4[2 * u + 1], (float)c2[u], -(float)s2[u]);
-            o4[2 * u] = rr[0];
-            o4[2 * u + 1] = rr[1];
-          }
-        }
-        *reinterpret_cast<bf16x4*>(qrow + 32 * db + 8 * r + 4 * hl) = o4;
-      }
-  }
-}
-
-// dK / dV (key-owned, no dQ): a workgroup owns 128 keys (4 waves x 32) and
-// walks the causal 64-query blocks.  Each wave keeps its 32 keys' K and V
-// MFMA operands in registers, computes S = Q K^T and dP = dO V^T with lane l
-// holding key l % 32, and accumulates dV^T += dO^T P and dK^T += Q^T dS in
-// registers (dO^T, Q^T from transposed reads).  The Q / dO blocks (swizzled
-// rows) and their lse * log2(e), Delta * scale rows (written by the dQ
-// kernel) are copied global -> LDS by the DMA path into two buffers, the
-// next block's copy running under this block's work: one barrier per block,
-// no staging registers, 34 KB of LDS, so two workgroups share a CU and their
-// phases interleave.  kRope: the dK epilogue applies the RoPE VJP (rcs / rsn:
-// tables [S][D/2]).
-template <bool kSeg, bool kRope>
-__global__ void __launch_bounds__(256, 2)
-    attn_dkdv64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse2,
-                       const float* __restrict__ dsc, const int32_t* __restrict__ seg, MutView dK, MutView dV, int B,
-                       int H, int S, float scale, float scale_log2, const bf16* __restrict__ rcs,
-                       const bf16* __restrict__ rsn) {
-  constexpr int D = 64, KC = 4, DB = 2, NK = 128;
-  __shared__ __attribute__((aligned(1024))) bf16 qg_s[2][2 * kBwdM * 64];  // [buffer][Q rows | dO rows]
-  __shared__ __attribute__((aligned(16))) float lse_s[2][kBwdM], dsc_s[2][kBwdM];
-  __shared__ int seg_s[2][kBwdM];
+__global__ void __launch_bounds__(kBwd64Threads, 2)
+    attn_bwd64_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
+                      const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
+                      MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2,
+                      const bf16* __restrict__ rcs, const bf16* __restrict__ rsn) {
+  constexpr int D = 64, KC = 4, DB = 2, NT = kBwd64Threads, NK = kBwd64Keys;
+  __shared__ __attribute__((aligned(16))) bf16 smem[(64 + 64 + 3 * NK) * 64];
+  __shared__ __attribute__((aligned(16))) float lse_s[kBwdM], delta_s[kBwdM];
+  __shared__ int seg_s[kBwdM];
+  // RoPE tables (cos, sin) of the workgroup's keys, read by the dK epilogue
+  // when the RoPE VJP is fused; staged here so their loads overlap the loop.
+  __shared__ __attribute__((aligned(16))) bf16 rope_s[2][NK * (D / 2)];
+  at64::lds_t* const Qs = gemm::lds_cast(smem);
+  at64::lds_t* const dOs = Qs + 64 * 64;
+  at64::lds_t* const Ks = dOs + 64 * 64;
+  at64::lds_t* const dSt = Ks + NK * 64;
+  at64::lds_t* const Vs = dSt + NK * 64;
 
   const int nkv = (S + NK - 1) / NK;
   int bh, kb;
   xcd_map(blockIdx.x, nkv, B * H, bh, kb);
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int k0 = kb * NK;
   const int kw0 = k0 + 32 * wave;
   const int my_k = kw0 + l32;
   const bool k_ok = my_k < S;
+
   const int seg_k = (kSeg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
 
-  // B operands of S = Q K^T and dP = dO V^T: key my_k, d = 16kc + 8hl .. +7.
-  bf16x8 kreg[KC], vreg[KC];
+  {
+    // (Branch-free, so these loads issue together with the K / V loads below.)
+    constexpr int kChunks = NK * (D / 2) / 8;  // 16-byte chunks per table
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    kreg[kc] = k_ok ? *reinterpret_cast<const bf16x8*>(K.row(b, h, my_k) + 16 * kc + 8 * hl) : bf16x8{};
-    vreg[kc] = k_ok ? *reinterpret_cast<const bf16x8*>(V.row(b, h, my_k) + 16 * kc + 8 * hl) : bf16x8{};
+    for (int r = 0; r < kChunks / NT; ++r) {
+      const int idx = tid + NT * r;
+      const int key = idx / (D / 16), c = idx % (D / 16);
+      const bool ok = rcs != nullptr && k0 + key < S;
+      const size_t off = ok ? (size_t)(k0 + key) * (D / 2) + 8 * c : 0;
+      *reinterpret_cast<bf16x8*>(&rope_s[0][8 * idx]) = ok ? *reinterpret_cast<const bf16x8*>(rcs + off) : bf16x8{};
+      *reinterpret_cast<bf16x8*>(&rope_s[1][8 * idx]) = ok ? *reinterpret_cast<const bf16x8*>(rsn + off) : bf16x8{};
+    }
+  }
+  // K and V tiles of the workgroup's keys (row-major, swizzled).  K feeds
+  // dQ = dS K (transposed reads) and, like V, the per-key MFMA operands of
+  // S = Q K^T and dP = dO V^T, which are re-read from LDS every step rather
+  // than held in 32 registers for the whole loop.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int idx = tid + NT * r;
+    const int row = idx >> 3, c = idx & 7;
+    const bool ok = k0 + row < S;
+    const bf16x8 kv = ok ? *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + row) + 8 * c) : bf16x8{};
+    const bf16x8 vv = ok ? *reinterpret_cast<const bf16x8*>(V.row(b, h, k0 + row) + 8 * c) : bf16x8{};
+    *(at64::lds_x8*)(Ks + at64::swz(row, c)) = kv;
+    *(at64::lds_x8*)(Vs + at64::swz(row, c)) = vv;
   }
 
   f32x16 dv_acc[DB], dk_acc[DB];
@@ -943,83 +796,95 @@ __global__ void __launch_bounds__(256, 2)
     dv_acc[db] = f32x16{};
     dk_acc[db] = f32x16{};
   }
-  // Per-(b, h) buffer resources: rows at or past S read as zeros.
+  // Per-(b, h) buffer resources: scalar bases, 32-bit per-lane offsets, and
+  // zeros / dropped writes past the end of the sequence instead of branches.
   const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(Q.row(b, h, 0), (uint32_t)(S * Q.ss * 2));
   const __amdgpu_buffer_rsrc_t g_rs = make_rsrc(dO.row(b, h, 0), (uint32_t)(S * dO.ss * 2));
-  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse2 + (size_t)bh * S, (uint32_t)S * 4u);
-  const __amdgpu_buffer_rsrc_t dsc_rs = make_rsrc(dsc + (size_t)bh * S, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (size_t)bh * S, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t delta_rs = make_rsrc(delta + (size_t)bh * S, (uint32_t)S * 4u);
   const __amdgpu_buffer_rsrc_t seg_rs =
-      make_rsrc(kSeg ? (const void*)(seg + (size_t)b * S) : (const void*)lse2, (uint32_t)S * 4u);
-  // Wave w copies 1 KB blocks 2w, 2w+1 (8 rows each) of the Q and dO blocks,
-  // in the swizzled row layout of attn64.h.
-  const int qss2 = (int)Q.ss * 2, gss2 = (int)dO.ss * 2;
-  int qoff[2], goff[2];
+      make_rsrc(kSeg ? (const void*)(seg + (size_t)b * S) : (const void*)lse, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t dq_rs = make_rsrc(dq_acc + (size_t)bh * S * D, (uint32_t)S * D * 4u);
+
+  // Register staging of one 64-query block: 16 B of Q and of dO per thread and step.
+  constexpr int QR = 64 * 8 / NT;
+  bf16x8 qst[QR], gst[QR];
+  float lse_st = 0.f, delta_st = 0.f;
+  int seg_st = 0;
+  auto load_q = [&](int qq0) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 8 * (2 * wave + j) + (lane >> 3);
-    const int t = (r >> 1) & 7;
-    const int c = (lane & 7) ^ (((t & 1) << 2) | (t >> 1));
-    qoff[j] = r * qss2 + 16 * c;
-    goff[j] = r * gss2 + 16 * c;
-  }
-  auto fill = [&](int buf, int qq0) {
-    at64::lds_t* const Qs = gemm::lds_cast(qg_s[buf]);
-    at64::lds_t* const dOs = Qs + kBwdM * 64;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int blk = 2 * wave + j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rs, (lds_void*)(Qs + blk * 512), 16, qoff[j] + qq0 * qss2, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rs, (lds_void*)(dOs + blk * 512), 16, goff[j] + qq0 * gss2, 0, 0, 0);
+    for (int r = 0; r < QR; ++r) {
+      const int idx = tid + NT * r;
+      const int qi = idx >> 3, c = idx & 7;
+      qst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              q_rs, ((qq0 + qi) * (int)Q.ss + 8 * c) * 2, 0, 0));
+      gst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              g_rs, ((qq0 + qi) * (int)dO.ss + 8 * c) * 2, 0, 0));
     }
-    if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(lse_rs, (lds_void*)&lse_s[buf][0], 4, (qq0 + lane) * 4, 0, 0, 0);
-    else if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dsc_rs, (lds_void*)&dsc_s[buf][0], 4, (qq0 + lane) * 4, 0, 0, 0);
-    else if (kSeg && wave == 2)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(seg_rs, (lds_void*)&seg_s[buf][0], 4, (qq0 + lane) * 4, 0, 0, 0);
+    if (tid < kBwdM) {
+      lse_st = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lse_rs, (qq0 + tid) * 4, 0, 0));
+      delta_st = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(delta_rs, (qq0 + tid) * 4, 0, 0));
+      if (kSeg) seg_st = (int)__builtin_amdgcn_raw_buffer_load_b32(seg_rs, (qq0 + tid) * 4, 0, 0);
+    }
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int idx = tid + NT * r;
+      const int qi = idx >> 3, c = idx & 7;
+      *(at64::lds_x8*)(Qs + at64::swz(qi, c)) = qst[r];
+      *(at64::lds_x8*)(dOs + at64::swz(qi, c)) = gst[r];
+    }
+    if (tid < kBwdM) {
+      // Scaled here, after (B), so the loads are not waited for at issue.
+      lse_s[tid] = lse_st * GPTRIG_LOG2E;
+      delta_s[tid] = delta_st * scale;  // dS = P * (scale*dP - scale*Delta)
+      if (kSeg) seg_s[tid] = seg_st;
+    }
   };
 
   const int qb_first = k0 / kBwdM;
   const int nqb = (S + kBwdM - 1) / kBwdM;
-  fill(0, qb_first * kBwdM);
+  load_q(qb_first * kBwdM);
+  store_q();
 
-  // One query block from LDS buffer `cur` (a compile-time index, so operand
-  // addresses are immediate offsets from one base).
-  auto step = [&](int qb, auto cur_tag) __attribute__((always_inline)) {
-    constexpr int cur = decltype(cur_tag)::value;
+  for (int qb = qb_first; qb < nqb; ++qb) {
     const int qq0 = qb * kBwdM;
-    // Block qb has landed in buffer `cur` (every wave waited for its own
-    // copies), and every wave is done with block qb - 1, so buffer cur ^ 1
-    // may be refilled.
-    GEMM_WAIT_VM0_LGKM0();
+    // (A) Q, dO, lse, delta of this block published.  Only LDS has to be
+    // complete here: the previous block's dQ atomics stay in flight.
+    GPTRIG_WAIT_LGKM0();
     wg_barrier();
-    if (qb + 1 < nqb) fill(cur ^ 1, qq0 + kBwdM);
-    const at64::lds_t* const Qs = gemm::lds_cast(qg_s[cur]);
-    const at64::lds_t* const dOs = Qs + kBwdM * 64;
-    const float* const ls = lse_s[cur];
-    const float* const dls = dsc_s[cur];
-    const int* const sgs = seg_s[cur];
+    // Prefetch the next block into registers; it is written to LDS after (B),
+    // once every wave is done with this block's Q / dO, ahead of the dQ
+    // atomics (so that wait never drains them).
+    // (The last block re-loads itself: the same code on every iteration.)
+    load_q(qb + 1 < nqb ? qq0 + kBwdM : qq0);
 
-    // One 32-query half of the block; kMask: the causal / ragged / segment
-    // mask per element (diagonal and edge blocks only).
+    const bool wave_active = kw0 <= qq0 + kBwdM - 1 && kw0 < S;
+    // One 32-query half of the block.  kMask: the causal / ragged / segment
+    // mask is evaluated per element (diagonal and edge blocks only); the
+    // interior blocks run a mask-free copy of the same code.
     auto qs_body = [&](int qs, auto mask_tag) {
       constexpr bool kMask = decltype(mask_tag)::value;
-      // (Unlike the mask-free copy, the masked one starts with a scheduling
-      // fence: with identical first instructions the two copies' operand
-      // reads are hoisted above the branch, and the longer live ranges spill.)
-      if constexpr (kMask) __builtin_amdgcn_sched_barrier(0);
+      bf16x8 qf[KC], gf[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        qf[kc] = at64::rowfrag(Qs, 32 * qs + l32, 2 * kc + hl);
+        gf[kc] = at64::rowfrag(dOs, 32 * qs + l32, 2 * kc + hl);
+      }
       f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        sacc = mfma32(at64::rowfrag(Qs, 32 * qs + l32, 2 * kc + hl), kreg[kc], sacc);
-        pacc = mfma32(at64::rowfrag(dOs, 32 * qs + l32, 2 * kc + hl), vreg[kc], pacc);
+        sacc = mfma32(qf[kc], at64::rowfrag(Ks, 32 * wave + l32, 2 * kc + hl), sacc);
+        pacc = mfma32(gf[kc], at64::rowfrag(Vs, 32 * wave + l32, 2 * kc + hl), pacc);
       }
       bf16x8 pb[2], db8[2];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int qr = 32 * qs + 8 * r + 4 * hl;
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&ls[qr]);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dls[qr]);
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse_s[qr]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&delta_s[qr]);
+        bf16x4 ds4;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int i = 4 * r + t;
@@ -1027,45 +892,75 @@ __global__ void __launch_bounds__(256, 2)
           if (kMask) {
             const int q = qq0 + qr + t;
             bool vis = my_k <= q && q < S && k_ok;
-            if (kSeg && vis) vis = sgs[qr + t] == seg_k;
+            if (kSeg && vis) vis = seg_s[qr + t] == seg_k;
             p = vis ? p : 0.f;
           }
+          const float ds = p * fmaf(pacc[i], scale, -d4[t]);
           pb[i >> 3][i & 7] = (bf16)p;
-          db8[i >> 3][i & 7] = (bf16)(p * fmaf(pacc[i], scale, -d4[t]));
+          const bf16 dsb = (bf16)ds;
+          db8[i >> 3][i & 7] = dsb;
+          ds4[t] = dsb;
         }
+        // dS^T row = this lane's key, queries 32qs + 8r + 4hl .. +3.
+        *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, 4 * qs + r) + 4 * hl) = ds4;
       }
-      // One 16-query chunk at a time, so at most 4 transposed operands are live.
+      bf16x8 gt[DB][2], qt[DB][2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        bf16x8 gt[DB], qt[DB];
+      for (int dbk = 0; dbk < DB; ++dbk)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          gt[dbk][c] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
+          qt[dbk][c] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
+        }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int dbk = 0; dbk < DB; ++dbk) {
-          gt[dbk] = at64::trfrag<true>(dOs, 32 * dbk, 32 * qs + 16 * c, lane);
-          qt[dbk] = at64::trfrag<true>(Qs, 32 * dbk, 32 * qs + 16 * c, lane);
+          dv_acc[dbk] = mfma32(gt[dbk][c], pb[c], dv_acc[dbk]);
+          dk_acc[dbk] = mfma32(qt[dbk][c], db8[c], dk_acc[dbk]);
         }
-#pragma unroll
-        for (int dbk = 0; dbk < DB; ++dbk) {
-          dv_acc[dbk] = mfma32(gt[dbk], pb[c], dv_acc[dbk]);
-          dk_acc[dbk] = mfma32(qt[dbk], db8[c], dk_acc[dbk]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
     };
-    if (kw0 <= qq0 + kBwdM - 1 && kw0 < S) {
-      if ((qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || kSeg) {
-        qs_body(0, std::true_type{});
-        __builtin_amdgcn_sched_barrier(0);
-        qs_body(1, std::true_type{});
-      } else {
-        qs_body(0, std::false_type{});
-        __builtin_amdgcn_sched_barrier(0);
-        qs_body(1, std::false_type{});
-      }
+    if (!wave_active) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, c) + 4 * hl) = bf16x4{};
+    } else if ((qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || kSeg) {
+      qs_body(0, std::true_type{});
+      __builtin_amdgcn_sched_barrier(0);  // keep the two halves' live ranges apart
+      qs_body(1, std::true_type{});
+    } else {
+      qs_body(0, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      qs_body(1, std::false_type{});
     }
-  };
-  for (int qb = qb_first; qb < nqb; qb += 2) {
-    step(qb, std::integral_constant<int, 0>{});
-    if (qb + 1 < nqb) step(qb + 1, std::integral_constant<int, 1>{});
+    GPTRIG_WAIT_LGKM0();
+    wg_barrier();  // (B) dS^T published; Q / dO / lse / delta of this block no longer read
+    store_q();
+
+    if (wave < 4) {  // dQ tile of this wave: queries 32*(wave/2).., d 32*(wave%2).. over all NK keys.
+      const int qs = wave >> 1, dblk = wave & 1;
+      // Two independent accumulation chains halve the dependent-MFMA latency.
+      f32x16 dqh[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+      for (int kq = 0; kq < NK / 64; ++kq) {
+        bf16x8 af[4], bfk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          af[j] = at64::trfrag<false>(dSt, 32 * qs, 16 * (4 * kq + j), lane);
+          bfk[j] = at64::trfrag<false>(Ks, 32 * dblk, 16 * (4 * kq + j), lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dqh[kq & 1] = mfma32(af[j], bfk[j], dqh[kq & 1]);
+      }
+      const f32x16 dq = dqh[0] + dqh[1];
+      // Row q = qq0 + 32qs + 4hl + 8(i/4) + i%4 of this lane's column; rows at
+      // or past S fall outside the buffer resource and are dropped.
+      const int voff = ((qq0 + 32 * qs + 4 * hl) * D + 32 * dblk + l32) * 4;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(dq[i], dq_rs, voff + (8 * (i >> 2) + (i & 3)) * D * 4, 0, 0);
+    }
+    // The next block's dS^T writes come after the next (A), which every wave
+    // reaches only after finishing this dQ step.
   }
 
   if (k_ok) {
@@ -1081,10 +976,10 @@ __global__ void __launch_bounds__(256, 2)
           v4[t] = (bf16)dv_acc[db][4 * r + t];
           k4[t] = (bf16)dk_acc[db][4 * r + t];
         }
-        if constexpr (kRope) {  // RoPE VJP: d = 32db + 8r + 4hl + t, pairs (t, t+1) for t = 0, 2
+        if (rcs) {  // RoPE VJP: d = 32db + 8r + 4hl + t, pairs (t, t+1) for t = 0, 2
           const int j0 = (32 * db + 8 * r + 4 * hl) / 2;
-          const bf16x2 c2 = *reinterpret_cast<const bf16x2*>(rcs + (size_t)my_k * (D / 2) + j0);
-          const bf16x2 s2 = *reinterpret_cast<const bf16x2*>(rsn + (size_t)my_k * (D / 2) + j0);
+          const bf16x2 c2 = *reinterpret_cast<const bf16x2*>(&rope_s[0][(32 * wave + l32) * (D / 2) + j0]);
+          const bf16x2 s2 = *reinterpret_cast<const bf16x2*>(&rope_s[1][(32 * wave + l32) * (D / 2) + j0]);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const bf16x2 rr = rope_pair((float)k4[2 * u], (float)k4[2 * u + 1], (float)c2[u], -(float)s2[u]);
@@ -1156,9 +1051,7 @@ int gptrig_attn_fwd(const void* q, const void* k, const void* v, const int32_t* 
 size_t gptrig_attn_bwd_workspace_bytes(int batch, int heads, int seq, int head_dim) {
   const size_t rows = (size_t)batch * heads * seq;
   const size_t delta = (rows * sizeof(float) + 255) & ~(size_t)255;
-  // head_dim 64: Delta * scale and lse * log2(e) rows; head_dim 128: Delta
-  // and the fp32 dQ accumulator.
-  return head_dim == 64 ? 2 * delta : delta + rows * head_dim * sizeof(float);
+  return delta + rows * head_dim * sizeof(float);
 }
 
 }  // extern "C"
@@ -1196,39 +1089,23 @@ int attn_bwd_impl(const void* q, const void* k, const void* v, const void* o, co
   const long long grid = (long long)batch * heads * nkv;
   const float sl2 = softmax_scale * GPTRIG_LOG2E;
   if (head_dim == 64) {
-    // The kernels address one (b, h) slice of Q / dO (dK/dV) and K / V (dQ)
-    // through 32-bit buffer offsets.
-    long long span = (long long)seq * (Q.ss > dO.ss ? Q.ss : dO.ss) * 2;
-    const long long kspan = (long long)seq * (K.ss > V.ss ? K.ss : V.ss) * 2;
-    if (kspan > span) span = kspan;
-    if (span >= (1ll << 31)) return GPTRIG_E_SHAPE;
-    const unsigned gq = (unsigned)((long long)batch * heads * ceil_div(seq, kBlockM));
-    const unsigned gk = (unsigned)((long long)batch * heads * ceil_div(seq, kBwdN));
-    // dQ first: it also writes the lse * log2(e) and Delta * scale rows the
-    // dK/dV kernel reads (workspace: Delta * scale, then lse * log2(e)).
-    float* lse2 = (float*)((char*)workspace + ((rows * sizeof(float) + 255) & ~(size_t)255));
-    if (segment_ids)
-      attn_dq64_kernel<true><<<gq, 256, 0, s>>>(Q, K, V, O, dO, lse, segment_ids, lse2, delta, dQ, batch, heads, seq,
-                                                softmax_scale, sl2, rcs, rsn);
-    else
-      attn_dq64_kernel<false><<<gq, 256, 0, s>>>(Q, K, V, O, dO, lse, nullptr, lse2, delta, dQ, batch, heads, seq,
-                                                 softmax_scale, sl2, rcs, rsn);
+    // The kernel addresses one (b, h) slice of Q / dO / dq_acc through 32-bit
+    // buffer offsets.
+    const long long span = (long long)seq * (Q.ss > dO.ss ? Q.ss : dO.ss) * 2;
+    if (span >= (1ll << 31) || (long long)seq * 64 * 4 >= (1ll << 31)) return GPTRIG_E_SHAPE;
+    attn_bwd_pre_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
+                                                                                seq);
     GPTRIG_CHECK_LAUNCH();
-    if (segment_ids) {
-      if (rcs)
-        attn_dkdv64_kernel<true, true><<<gk, 256, 0, s>>>(Q, K, V, dO, lse2, delta, segment_ids, dK, dV, batch, heads,
-                                                          seq, softmax_scale, sl2, rcs, rsn);
-      else
-        attn_dkdv64_kernel<true, false><<<gk, 256, 0, s>>>(Q, K, V, dO, lse2, delta, segment_ids, dK, dV, batch,
-                                                           heads, seq, softmax_scale, sl2, nullptr, nullptr);
-    } else {
-      if (rcs)
-        attn_dkdv64_kernel<false, true><<<gk, 256, 0, s>>>(Q, K, V, dO, lse2, delta, nullptr, dK, dV, batch, heads,
-                                                           seq, softmax_scale, sl2, rcs, rsn);
-      else
-        attn_dkdv64_kernel<false, false><<<gk, 256, 0, s>>>(Q, K, V, dO, lse2, delta, nullptr, dK, dV, batch, heads,
-                                                            seq, softmax_scale, sl2, nullptr, nullptr);
-    }
+    const unsigned grid64 = (unsigned)((long long)batch * heads * ceil_div(seq, kBwd64Keys));
+    if (segment_ids)
+      attn_bwd64_kernel<true><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV,
+                                                               batch, heads, seq, softmax_scale, sl2, rcs, rsn);
+    else
+      attn_bwd64_kernel<false><<<grid64, kBwd64Threads, 0, s>>>(Q, K, V, dO, lse, delta, nullptr, dq_acc, dK, dV,
+                                                                batch, heads, seq, softmax_scale, sl2, rcs, rsn);
+    GPTRIG_CHECK_LAUNCH();
+    attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq,
+                                                                                   rcs, rsn);
   } else {
     attn_bwd_pre_kernel<128><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
                                                                                  seq);

@@ -40,10 +40,10 @@ class AttentionTiles:
     block_kv_compute: int = 32  # forward: keys per online-softmax half-step
     block_q_dkv: int = 64  # backward: queries per step
     block_q_dkv_compute: int = 32
-    block_kv_dkv: int = 128  # dK/dV: keys per workgroup (4 waves x 32)
+    block_kv_dkv: int = 256  # backward: keys per workgroup (8 waves x 32)
     block_kv_dkv_compute: int = 32
-    block_q_dq: int = 128  # dQ: queries per workgroup (4 waves x 32), its own pass
-    block_kv_dq: int = 64  # dQ: keys per LDS tile
+    block_q_dq: int = 64  # dQ is accumulated by the same (key-owned) workgroups
+    block_kv_dq: int = 256
     block_kv_dq_compute: int = 32
 
     @property
@@ -56,14 +56,13 @@ class AttentionTiles:
 
 def kernel_tiles(head_dim: int) -> AttentionTiles:
     """The plan the kernels run for ``head_dim`` (padded up to 64 or 128):
-    the head_dim 128 backward owns 128 keys per workgroup (4 waves x 32) and
-    accumulates dQ in those key-owned workgroups (64 queries per step)."""
+    the head_dim 128 backward owns 128 keys per workgroup (4 waves x 32)."""
 
     if head_dim <= 0 or head_dim > _KERNEL_DIMS[-1]:
         raise ValueError(f"head_dim must be in (0, {_KERNEL_DIMS[-1]}]; got {head_dim}")
     if head_dim <= 64:
         return AttentionTiles()
-    return AttentionTiles(block_q_dq=64, block_kv_dq=128)
+    return AttentionTiles(block_kv_dkv=128, block_kv_dq=128)
 
 
 def attention_tile_candidates(*, sequence: int, head_dim: int, training: bool = True) -> tuple[AttentionTiles, ...]:

@@ -142,8 +142,7 @@ def test_attention_tile_plan_describes_the_kernels():
     from gptrig.kernels.flash_attention import kernel_tiles
 
     assert select_attention_tiles(sequence=1024, head_dim=64) == AttentionTiles()
-    assert kernel_tiles(64).block_kv_dkv == 128 and kernel_tiles(64).block_q_dq == 128
-    assert kernel_tiles(128).block_kv_dq == 128 and kernel_tiles(128).block_q_dq == 64
+    assert kernel_tiles(64).block_kv_dkv == 256 and kernel_tiles(128).block_kv_dkv == 128
     assert kernel_tiles(48) == kernel_tiles(64) and kernel_tiles(96) == kernel_tiles(128)
     q = torch.zeros((1, 2, 16, 64), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="fixed tile plan"):
