@@ -30,7 +30,10 @@
 
 #include <math.h>
 
+#include <algorithm>
+#include <functional>
 #include <mutex>
+#include <vector>
 
 namespace {
 
@@ -108,7 +111,12 @@ __device__ __forceinline__ float2 column_stats_keep(f32x16 (&acc)[4][2], int nb,
         const int r0 = 32 * mb + 8 * q;  // rows r0 .. r0 + 3 of the lane's block
         f16* dst = col + (r0 / 4) * 128;
         if (!kMask || r0 + 3 < vlim) {
-          *reinterpret_cast<f16x4*>(dst) = p4;
+          // Streaming store: the kept array is read back by the next launch,
+          // not by this one (measured 7% faster for this launch at 65536
+          // tokens than a plain store, which competes with the operand slabs
+          // for L2).
+          __builtin_nontemporal_store(__builtin_bit_cast(unsigned long long, p4),
+                                      reinterpret_cast<unsigned long long*>(dst));
         } else {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
@@ -451,15 +459,11 @@ __global__ void __launch_bounds__(gemm::THREADS)
 // K range of B(k, n), computed from the B fragments already in registers and shared out
 // over the M tiles (the bias gradient of a linear layer, fused into its
 // weight gradient).
+// One workgroup's tile (tm, tn) of that product over [k_begin, k_end).
 template <bool AK, bool BKM>
-__global__ void __launch_bounds__(gemm::THREADS)
-    gemm_f32_kernel(Operand A, Operand B, int M, int N, int K, int ksplit, float* __restrict__ C, int64_t ldc,
-                    int mode, float* __restrict__ colsum) {
-  int tm, tn, split;
-  gemm::split_tile_coords(blockIdx.x, gridDim.x, M, N, tm, tn, split);
-  const int kslice = ((K + ksplit - 1) / ksplit + gemm::BK - 1) / gemm::BK * gemm::BK;
-  const int k_begin = split * kslice;
-  const int k_end = min(K, k_begin + kslice);
+__device__ __forceinline__ void gemm_f32_tile(Operand A, Operand B, int M, int N, int k_begin, int k_end, int tm,
+                                              int tn, float* __restrict__ C, int64_t ldc, int mode,
+                                              float* __restrict__ colsum) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   f32x16 acc[4][2];
   float csum[2] = {0.f, 0.f};
@@ -508,6 +512,52 @@ __global__ void __launch_bounds__(gemm::THREADS)
         }
       }
     }
+  }
+}
+
+// K range [k_begin, k_end) of split `split` when K is cut into ksplit slices of whole stages.
+__device__ __forceinline__ void split_range(int K, int ksplit, int split, int& k_begin, int& k_end) {
+  const int kslice = ((K + ksplit - 1) / ksplit + gemm::BK - 1) / gemm::BK * gemm::BK;
+  k_begin = split * kslice;
+  k_end = min(K, k_begin + kslice);
+}
+
+template <bool AK, bool BKM>
+__global__ void __launch_bounds__(gemm::THREADS)
+    gemm_f32_kernel(Operand A, Operand B, int M, int N, int K, int ksplit, float* __restrict__ C, int64_t ldc,
+                    int mode, float* __restrict__ colsum) {
+  int tm, tn, split, k_begin, k_end;
+  gemm::split_tile_coords(blockIdx.x, gridDim.x, M, N, tm, tn, split);
+  split_range(K, ksplit, split, k_begin, k_end);
+  gemm_f32_tile<AK, BKM>(A, B, M, N, k_begin, k_end, tm, tn, C, ldc, mode, colsum);
+}
+
+// The two gradient GEMMs of the kept-softmax backward in one launch, so that
+// neither leaves the GPU part-empty while the other waits behind it:
+//   dh (+)= G W   A(m = token, k = v) = G^T blocked (MN-major), B = W [V][d] (MN-major),
+//                 split over the vocabulary into dh_split slices (fp32 atomics, or a plain
+//                 store with one slice);
+//   dW (+)= G^T h A = G^T blocked (K-major), B = h [n][d] (MN-major), split over the tokens
+//                 into dw_split slices (mode dw_mode).
+// Workgroups [0, first) run the items of the group with the longer items
+// (dh_first: the dh items), the rest the other group's: the dispatcher hands
+// the long items out first and the short ones fill the CUs that free up.
+__global__ void __launch_bounds__(gemm::THREADS)
+    flce_keep_gemms_kernel(Operand Gt, Operand Wv, Operand Hd, int n, int d, int vc, int dh_split, int dw_split,
+                           float* __restrict__ dh_acc, int dh_mode, float* __restrict__ dw, int dw_mode, int n_dh,
+                           int n_dw, bool dh_first) {
+  const int b = blockIdx.x;
+  const bool is_dh = dh_first ? b < n_dh : b >= n_dw;
+  const int pid = dh_first ? (is_dh ? b : b - n_dh) : (is_dh ? b - n_dw : b);
+  int tm, tn, split, k_begin, k_end;
+  if (is_dh) {
+    gemm::split_tile_coords(pid, n_dh, n, d, tm, tn, split);
+    split_range(vc, dh_split, split, k_begin, k_end);
+    gemm_f32_tile<false, false>(Gt, Wv, n, d, k_begin, k_end, tm, tn, dh_acc, d, dh_mode, nullptr);
+  } else {
+    gemm::split_tile_coords(pid, n_dw, vc, d, tm, tn, split);
+    split_range(n, dw_split, split, k_begin, k_end);
+    gemm_f32_tile<true, false>(Gt, Hd, vc, d, k_begin, k_end, tm, tn, dw, d, dw_mode, nullptr);
   }
 }
 
@@ -948,25 +998,78 @@ int gptrig_flce_fwd_keep(const void* hidden, const void* weight, const int32_t* 
 
 namespace {
 
-// Token split of the kept-softmax dW GEMM (tiles 256x256 output tiles over
-// k_iters 32-token stages), from an estimate in units of one stage: each round
-// of CU-sized waves costs its stages plus its epilogue, about 60 stages for a
-// split's fp32 atomic add of a 256 KB tile into the large dW array, 20 for a
-// read-modify-write and 10 for a plain store (measured at 5120 and 65536
-// tokens per call).
-int dweight_split(unsigned tiles, int k_iters, bool accumulate) {
+// Work split of flce_keep_gemms_kernel, chosen by simulating the
+// dispatcher: the items (dh tiles x dh_split, dW tiles x dw_split) are handed
+// out in launch order to whichever CU frees up first, each costing its
+// 32-deep stages (rounded up to the main loop's groups of four) plus its
+// epilogue, in units of one stage: about 60 for an fp32 atomic add of a 256 KB
+// tile into a large array, 20 for a read-modify-write and 10 for a plain store
+// (measured at 5120 and 65536 tokens per call).  The plan with the shortest
+// estimated makespan wins; plans are cached per shape.
+struct KeepPlan {
+  int dh_split, dw_split, dh_mode, dw_mode;
+  bool dh_first;
+};
+
+double keep_makespan(int cus, unsigned dh_tiles, int dh_k, int dh_split, double dh_epi, unsigned dw_tiles, int dw_k,
+                     int dw_split, double dw_epi, bool& dh_first) {
+  auto len = [](int k_iters, int split) {
+    const int per = ceil_div(k_iters, split);
+    return (double)((per + 3) & ~3);
+  };
+  const double l_dh = len(dh_k, dh_split) + dh_epi, l_dw = len(dw_k, dw_split) + dw_epi;
+  dh_first = l_dh >= l_dw;
+  const double l1 = dh_first ? l_dh : l_dw, l2 = dh_first ? l_dw : l_dh;
+  const int64_t k1 = (int64_t)(dh_first ? dh_tiles * dh_split : dw_tiles * dw_split);
+  const int64_t k2 = (int64_t)(dh_first ? dw_tiles * dw_split : dh_tiles * dh_split);
+  // Min-heap of CU free times (all items of a group have one length).
+  std::vector<double> heap((size_t)cus, 0.0);
+  auto take = [&](double l) {
+    std::pop_heap(heap.begin(), heap.end(), std::greater<double>());
+    heap.back() += l;
+    std::push_heap(heap.begin(), heap.end(), std::greater<double>());
+  };
+  for (int64_t i = 0; i < k1; ++i) take(l1);
+  for (int64_t i = 0; i < k2; ++i) take(l2);
+  return *std::max_element(heap.begin(), heap.end());
+}
+
+KeepPlan keep_plan(int n, int d, int vocab, bool accumulate) {
+  struct Entry {
+    int dev, n, d, vocab;
+    bool acc;
+    KeepPlan plan;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+      if (e.dev == dev && e.n == n && e.d == d && e.vocab == vocab && e.acc == accumulate) return e.plan;
+  }
   const int cus = gemm::device_cus();
-  int best = 1;
+  const unsigned dh_tiles = tiles_of(n, d), dw_tiles = tiles_of(vocab, d);
+  const int dh_k = ceil_div(vocab, gemm::BK), dw_k = ceil_div(n, gemm::BK);
+  KeepPlan best{1, 1, 0, accumulate ? 1 : 0, true};
   double best_cost = 1e300;
-  for (int sp = 1; sp <= 16 && (sp == 1 || k_iters / sp >= 8); ++sp) {
-    const double rounds = (double)ceil_div((int64_t)tiles * sp, (int64_t)cus);
-    const double epi = sp > 1 ? 60.0 : (accumulate ? 20.0 : 10.0);
-    const double cost = rounds * ((double)ceil_div(k_iters, sp) + epi);
-    if (cost < best_cost * 0.999) {
-      best_cost = cost;
-      best = sp;
+  static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+  for (int sh : kSplits) {
+    if (sh > 1 && dh_k / sh < 8) break;
+    for (int sw : kSplits) {
+      if (sw > 1 && dw_k / sw < 8) break;
+      bool dh_first;
+      const double cost = keep_makespan(cus, dh_tiles, dh_k, sh, sh > 1 ? 60.0 : 10.0, dw_tiles, dw_k, sw,
+                                        sw > 1 ? 60.0 : (accumulate ? 20.0 : 10.0), dh_first);
+      if (cost < best_cost * 0.999) {
+        best_cost = cost;
+        best = KeepPlan{sh, sw, sh > 1 ? 2 : 0, sw > 1 ? 2 : (accumulate ? 1 : 0), dh_first};
+      }
     }
   }
+  std::lock_guard<std::mutex> lock(mu);
+  cache.push_back(Entry{dev, n, d, vocab, accumulate, best});
   return best;
 }
 
@@ -1156,19 +1259,18 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
   float* dh_acc = (float*)workspace;
   const bf16* Wp = (const bf16*)weight;
   const bf16* Hp = (const bf16*)hidden;
-  // dW = G^T h over this call's n tokens: split over the tokens (fp32 atomics)
-  // only when that beats one workgroup per output tile (plain store, or
-  // read-modify-write when accumulating).  With few tokens per call (a token
-  // chunk of a bounded run) the split's atomic epilogues dominate.
+  // dW (+)= G^T h and dh = G W over this call's n tokens in one launch
+  // (flce_keep_gemms_kernel), split as keep_plan estimates fastest.  With few
+  // tokens per call (a token chunk of a bounded run) the dW tiles are short and
+  // the dh tiles long; with many, both are long enough to need no split.
   const int vc = vocab;
-  const int dw_split = dweight_split(tiles_of(vc, d), ceil_div(n, gemm::BK), accumulate_dweight != 0);
-  const int dw_mode = dw_split > 1 ? 2 : (accumulate_dweight ? 1 : 0);
-  if (!accumulate_dweight && dw_split > 1) {
+  const KeepPlan plan = keep_plan(n, d, vocab, accumulate_dweight != 0);
+  if (!accumulate_dweight && plan.dw_mode == 2) {
     const int64_t total = (int64_t)vocab * d;
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dweight, total);
     GPTRIG_CHECK_LAUNCH();
   }
-  {
+  if (plan.dh_mode == 2) {
     const int64_t total = (int64_t)n * d;
     zero_f32_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, total);
     GPTRIG_CHECK_LAUNCH();
@@ -1181,15 +1283,11 @@ int gptrig_flce_bwd_keep(const void* hidden, const void* weight, const int32_t* 
   flce_keep_rescale_kernel<<<rgrid, 256, 0, s>>>(gt, alpha, n, vocab, semantic_vocab, targets, cotangent,
                                                   cotangent_scale);
   GPTRIG_CHECK_LAUNCH();
-  // dW (+)= G^T h and dh += G W.
-  Operand Ag{gt, n, keep_rows(vocab)}, Bh{Hp, d};
-  gemm_f32_kernel<true, false><<<tiles_of(vc, d) * dw_split, gemm::THREADS, 0, s>>>(Ag, Bh, vc, d, n, dw_split,
-                                                                                      dweight, d, dw_mode, nullptr);
-  GPTRIG_CHECK_LAUNCH();
-  Operand Agt{gt, n, keep_rows(vocab)}, Bw{Wp, d};
-  const int dh_split = gemm::choose_split(tiles_of(n, d), ceil_div(vc, gemm::BK));
-  gemm_f32_kernel<false, false><<<tiles_of(n, d) * dh_split, gemm::THREADS, 0, s>>>(Agt, Bw, n, d, vc, dh_split,
-                                                                                      dh_acc, d, 2, nullptr);
+  const unsigned n_dh = tiles_of(n, d) * (unsigned)plan.dh_split;
+  const unsigned n_dw = tiles_of(vc, d) * (unsigned)plan.dw_split;
+  flce_keep_gemms_kernel<<<n_dh + n_dw, gemm::THREADS, 0, s>>>(
+      Operand{gt, n, keep_rows(vocab)}, Operand{Wp, d}, Operand{Hp, d}, n, d, vc, plan.dh_split, plan.dw_split, dh_acc,
+      plan.dh_mode, dweight, plan.dw_mode, (int)n_dh, (int)n_dw, plan.dh_first);
   GPTRIG_CHECK_LAUNCH();
   const int64_t total = (int64_t)n * d;
   f32_to_bf16_kernel<<<ceil_div(ceil_div(total, 4), 256), 256, 0, s>>>(dh_acc, (bf16*)dhidden, total);
