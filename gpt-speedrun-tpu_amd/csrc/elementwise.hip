@@ -311,6 +311,82 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd8_kernel(const bf16* __restric
     partial[(size_t)blockIdx.x * d + j] = red[0][j] + red[1][j] + red[2][j] + red[3][j];
 }
 
+// Row width a multiple of 256 (at most 1024): one half-wave per row, lane l
+// of the half holding chunks l, l + 32, ... of 8 elements, so every lane
+// carries C chunks (with a wave per row, d = 768 left half the lanes idle on
+// the second chunk, and the VALU work of that chunk cost a full-width
+// instruction).  The two halves of a wave take consecutive rows; per-row sums
+// reduce over the 32 lanes of a half.  Same arithmetic and rounding as
+// rmsnorm_bwd8_kernel.
+template <int C>
+__global__ void __launch_bounds__(256) rmsnorm_bwd_hw_kernel(const bf16* __restrict__ dy, const bf16* __restrict__ x,
+                                                             const bf16* __restrict__ scale,
+                                                             const float* __restrict__ rstd,
+                                                             const bf16* __restrict__ dres, bf16* __restrict__ dx,
+                                                             float* __restrict__ partial, int rows, int d) {
+  __shared__ float red[8][C * 256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  float dsc[C][8];
+  bf16x8 sv[C];
+#pragma unroll
+  for (int t = 0; t < C; ++t) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dsc[t][j] = 0.f;
+    sv[t] = *reinterpret_cast<const bf16x8*>(scale + 8 * (l32 + 32 * t));
+  }
+  // Row pair p (uniform per wave) covers rows 2p and 2p + 1.
+  const int pstride = gridDim.x * 4;
+  for (int p = blockIdx.x * 4 + wave; 2 * p < rows; p += pstride) {
+    const int row = 2 * p + hl;
+    const bool ok = row < rows;
+    bf16x8 xv[C], gv[C], rv[C];
+    const float r = ok ? rstd[row] : 0.f;
+#pragma unroll
+    for (int t = 0; t < C; ++t) {
+      const size_t o = (size_t)(ok ? row : 0) * d + 8 * (l32 + 32 * t);
+      xv[t] = ok ? __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(x + o)) : bf16x8{};
+      gv[t] = ok ? __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(dy + o)) : bf16x8{};
+      if (dres) rv[t] = ok ? __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(dres + o)) : bf16x8{};
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int t = 0; t < C; ++t)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dot += (float)(bf16)((float)gv[t][j] * (float)sv[t][j]) * (float)xv[t][j];
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+    const float coef = r * r * r * dot / (float)d;
+    if (ok) {
+#pragma unroll
+      for (int t = 0; t < C; ++t) {
+        bf16x8 ov;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xf = (float)xv[t][j], g = (float)gv[t][j];
+          const float dn = (float)(bf16)(g * (float)sv[t][j]);
+          float v = (float)(bf16)(r * dn - coef * xf);
+          if (dres) v += (float)rv[t][j];
+          ov[j] = (bf16)v;
+          dsc[t][j] += g * (float)(bf16)(xf * r);
+        }
+        *reinterpret_cast<bf16x8*>(dx + (size_t)row * d + 8 * (l32 + 32 * t)) = ov;
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < C; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[2 * wave + hl][8 * (l32 + 32 * t) + j] = dsc[t][j];
+  __syncthreads();
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    float acc = 0.f;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) acc += red[h][j];
+    partial[(size_t)blockIdx.x * d + j] = acc;
+  }
+}
+
 __global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict__ partial, int parts, int d,
                                                          float* __restrict__ out) {
   __shared__ float red[4][64];
@@ -795,7 +871,17 @@ int gptrig_rmsnorm_bwd(const void* dy, const void* x, const void* scale, const f
     GPTRIG_CHECK_LAUNCH();
   }
   const int c8 = ceil_div(d / 8, 64);
-  if (d % 8 == 0 && c8 <= kMaxC8) {
+  if (d % 256 == 0 && d <= 1024) {
+    const int c = d / 256;
+#define GPTRIG_RMSHW(C)                                                                                           \
+  rmsnorm_bwd_hw_kernel<C><<<blocks, 256, 0, s>>>((const bf16*)dy, (const bf16*)x, (const bf16*)scale, rstd,        \
+                                                  (const bf16*)dresidual, (bf16*)dx, (float*)workspace, rows, d)
+    if (c == 1) GPTRIG_RMSHW(1);
+    else if (c == 2) GPTRIG_RMSHW(2);
+    else if (c == 3) GPTRIG_RMSHW(3);
+    else GPTRIG_RMSHW(4);
+#undef GPTRIG_RMSHW
+  } else if (d % 8 == 0 && c8 <= kMaxC8) {
 #define GPTRIG_RMS8(C)                                                                                          \
   rmsnorm_bwd8_kernel<C><<<blocks, 256, 0, s>>>((const bf16*)dy, (const bf16*)x, (const bf16*)scale, rstd,        \
                                                 (const bf16*)dresidual, (bf16*)dx, (float*)workspace, rows, d)

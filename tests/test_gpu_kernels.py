@@ -271,6 +271,33 @@ def test_rmsnorm_forward_backward():
     assert maxabs(sg.grad, sr.grad) <= 1e-2 * float(sr.grad.abs().max())
 
 
+@pytest.mark.parametrize("rows,d", [(1, 768), (333, 768), (333, 256), (200, 512), (201, 1024), (333, 320), (65, 2048)])
+def test_rmsnorm_backward_widths_with_residual_gradient(rows, d):
+    """The RMSNorm backward at the widths of each kernel form (a half-wave per
+    row for d a multiple of 256 up to 1024, a wave per row otherwise), odd
+    row counts, the fused residual-gradient add and an accumulated dscale,
+    against the oracle's rms_norm VJP (rig/nn.py:26-33) plus the residual
+    gradient."""
+    from gptrig import nn as gnn
+
+    print(f"rmsnorm backward rows={rows} d={d}", flush=True)
+    x = randn((rows, d), 57, 2.0)
+    scale = (1.0 + 0.1 * randn((d,), 58, 1.0, torch.float32))
+    dy = randn((rows, d), 59)
+    dres = randn((rows, d), 60)
+    xr = x.clone().requires_grad_(True)
+    sr = scale.clone().requires_grad_(True)
+    onn.rms_norm(xr, sr, torch.bfloat16).backward(dy)
+    want_dx = (xr.grad.float() + dres.float()).to(torch.bfloat16)
+    sc = scale.to(torch.bfloat16).to(DEV)
+    xd = x.to(DEV)
+    _, rstd = gnn.rmsnorm_forward(xd, sc)
+    base = torch.full((d,), 0.25, dtype=torch.float32, device=DEV)
+    dx, dscale = gnn.rmsnorm_backward(dy.to(DEV), xd, sc, rstd, dscale=base, accumulate=True, dresidual=dres.to(DEV))
+    assert maxabs(dx, want_dx) <= 2e-2 * float(want_dx.float().abs().max())
+    assert maxabs(dscale - 0.25, sr.grad) <= 1e-2 * float(sr.grad.abs().max())
+
+
 @pytest.mark.parametrize("branch_scale", [1.0, 0.5 ** 0.5])
 def test_add_rmsnorm_matches_add_then_norm(branch_scale):
     """The fused residual add + norm equals the oracle's residual add
