@@ -256,10 +256,11 @@ __device__ __forceinline__ void lse_fold(float& m, float& s, float pm, float ps)
   m = m2;
 }
 
-// 64 tokens per workgroup (lane = token), each of the 4 waves folding every
-// fourth tile, the 4 partial pairs then folded through LDS: 16 waves per CU
-// with independent loads instead of one serial chain per token.
-constexpr int kCombineWaves = 4;
+// 64 tokens per workgroup (lane = token), each of the kCombineWaves waves
+// folding every kCombineWaves-th tile, the partial pairs then folded through
+// LDS: many waves per CU with independent loads instead of one serial chain
+// per token.
+template <int kCombineWaves>
 __global__ void __launch_bounds__(64 * kCombineWaves)
     flce_combine_kernel(const float2* __restrict__ partial, int ntiles, int N, int sem_v,
                         const int32_t* __restrict__ targets, const float* __restrict__ tlogit,
@@ -1095,8 +1096,15 @@ int flce_fwd_launch(const void* hidden, const void* weight, const int32_t* targe
   flce_target_logit_kernel<<<ceil_div(n, 4), 256, 0, s>>>((const bf16*)hidden, (const bf16*)weight, targets, n, d,
                                                            semantic_vocab, tlogit);
   GPTRIG_CHECK_LAUNCH();
-  flce_combine_kernel<<<ceil_div(n, 64), 64 * kCombineWaves, 0, s>>>(partial, ntiles, n, semantic_vocab, targets,
-                                                                      tlogit, lse, losses);
+  // 4 waves per 64 tokens; 16 when that leaves the grid short of the CUs
+  // (a token chunk of a bounded run: each wave then folds a quarter as many
+  // tiles, and the launch is latency-bound, not bandwidth-bound).
+  if (ceil_div(n, 64) < gemm::device_cus())
+    flce_combine_kernel<16><<<ceil_div(n, 64), 64 * 16, 0, s>>>(partial, ntiles, n, semantic_vocab, targets, tlogit,
+                                                                lse, losses);
+  else
+    flce_combine_kernel<4><<<ceil_div(n, 64), 64 * 4, 0, s>>>(partial, ntiles, n, semantic_vocab, targets, tlogit,
+                                                              lse, losses);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
