@@ -47,6 +47,10 @@ using gemm::Operand;
 // lim are padding (-inf); the unmasked copy has no per-element compare.
 template <bool kMask>
 __device__ __forceinline__ float2 column_stats(f32x16 (&acc)[4][2], int nb, int lim) {
+  // The masked copy takes lim through an empty asm, so its 64 row compares
+  // stay inside the (rarely taken) masked branch: hoisted above it, they ran
+  // for every tile and their 64-bit results spilled to VGPR lanes.
+  if (kMask) asm volatile("" : "+v"(lim));
   float mx = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
@@ -85,6 +89,7 @@ typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 // Nothing is stored for a column with no real row.
 template <bool kMask>
 __device__ __forceinline__ float2 column_stats_keep(f32x16 (&acc)[4][2], int nb, int lim, int vlim, f16* col) {
+  if (kMask) asm volatile("" : "+v"(lim), "+v"(vlim));  // (see column_stats)
   float mx = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
