@@ -40,7 +40,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # `rocprofv3 --pmc` runs of `bench.py --traffic-pass`; the per-launch table and
 # commands are in profiles/flce_traffic_config_d.md.  Re-measure after kernel
 # changes; a shape without a measurement reports null.
-FLCE_TRAFFIC_BYTES = {(65536, 5056): (37687 + 15519) * 2 ** 20, (65536, 65536): (32786 + 13751) * 2 ** 20}
+FLCE_TRAFFIC_BYTES = {(65536, 5056): (37537 + 15518) * 2 ** 20, (65536, 65536): (32550 + 13751) * 2 ** 20}
 
 
 def parse_args():
