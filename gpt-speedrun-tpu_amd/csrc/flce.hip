@@ -23,9 +23,13 @@
 //            from one half and K1 of chunk c into the other, its workgroups
 //            taking items from per-XCD token-block counters and never
 //            waiting for one another (the stream orders the launches).
-//   kept-softmax forward / backward: the forward also stores fp16
-//            exp(logit - max) in the blocked G^T layout; the backward
-//            rescales it in place to G instead of recomputing the logits.
+//   kept-softmax forward / backward (a token chunk at a time, its kept
+//            buffer bounded by the caller): the forward also stores fp16
+//            exp(logit - max) in 4-row x 32-token groups; the backward
+//            rescales them in place to the blocked G^T (no logits recompute)
+//            and runs dW (+)= G^T h and dh = G W in one launch
+//            (flce_keep_gemms_kernel), split as a host simulation of the
+//            dispatch estimates fastest.
 #include "gemm_core.h"
 
 #include <math.h>
