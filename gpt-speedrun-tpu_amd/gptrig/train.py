@@ -389,13 +389,25 @@ class GPTTrainer:
         dgate = torch.empty(R, dtype=F32, device=dev)
         _lib.call("gptrig_moe_combine_bwd", dm.data_ptr(), out.data_ptr(), position.data_ptr(), gate.data_ptr(),
                   dout.data_ptr(), dgate.data_ptr(), N, d, k, s)
-        _lib.call("gptrig_moe_gmm_dw", hidden.data_ptr(), eh, dout.data_ptr(), d, counts.data_ptr(),
-                  A.grad(p + "expert_down_w").data_ptr(), A.grad(p + "expert_down_b").data_ptr(), R, eh, d, E, s)
         dpre = torch.empty((R, eh), dtype=BF16, device=dev)
         _lib.call("gptrig_moe_gmm", dout.data_ptr(), d, A.w(p + "expert_down_w").data_ptr(), 1, counts.data_ptr(),
                   None, 2, dpre.data_ptr(), pre.data_ptr(), eh, R, d, eh, E, s)
-        _lib.call("gptrig_moe_gmm_dw", grouped.data_ptr(), d, dpre.data_ptr(), eh, counts.data_ptr(),
-                  A.grad(p + "expert_up_w").data_ptr(), A.grad(p + "expert_up_b").data_ptr(), R, d, eh, E, s)
+        # The expert weight gradients go to the weight-gradient stream, like
+        # the dense linears': they overlap the rest of this block's backward
+        # and the blocks below.  Their inputs are per-call tensors, so each
+        # is marked as in use by that stream (the allocator then reuses none
+        # of them before the stream's kernels have run).
+        main, side = torch.cuda.current_stream(dev), self.wgrad_stream
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            ws = _lib.stream()
+            _lib.call("gptrig_moe_gmm_dw", hidden.data_ptr(), eh, dout.data_ptr(), d, counts.data_ptr(),
+                      A.grad(p + "expert_down_w").data_ptr(), A.grad(p + "expert_down_b").data_ptr(), R, eh, d, E,
+                      ws)
+            _lib.call("gptrig_moe_gmm_dw", grouped.data_ptr(), d, dpre.data_ptr(), eh, counts.data_ptr(),
+                      A.grad(p + "expert_up_w").data_ptr(), A.grad(p + "expert_up_b").data_ptr(), R, d, eh, E, ws)
+        for t in (hidden, dout, grouped, dpre, counts):
+            t.record_stream(side)
         dgrouped = torch.empty((R, d), dtype=BF16, device=dev)
         _lib.call("gptrig_moe_gmm", dpre.data_ptr(), eh, A.w(p + "expert_up_w").data_ptr(), 1, counts.data_ptr(),
                   None, 0, dgrouped.data_ptr(), None, d, R, eh, d, E, s)
