@@ -13,12 +13,15 @@
 // row max/sum are lane-local (+ one xor-32 exchange) and P^T is already the
 // B operand of O^T = V^T P^T, so probabilities never leave registers.
 //
-// Backward mapping: a workgroup owns 128 keys (4 waves x 32) and walks the
-// causal query blocks (64 queries per step).  Each wave computes S = Q K^T and
-// dP = dO V^T with lane l holding key l%32, accumulates dV^T += dO^T P and
-// dK^T += Q^T dS in registers, and publishes bf16 dS to LDS; the workgroup
-// then forms dQ = dS K (all 128 keys) and adds it to an fp32 accumulator with
-// atomics.  A last pass rounds dQ to bf16.
+// Backward mapping (KV-owned): a workgroup owns a block of keys and walks
+// the causal query blocks (64 queries per step).  Each wave computes S = Q K^T
+// and dP = dO V^T with lane l holding key l%32, accumulates dV^T += dO^T P and
+// dK^T += Q^T dS in registers, and publishes bf16 dS to LDS; dQ = dS K over
+// the workgroup's keys is added to an fp32 accumulator with atomics, and a
+// last pass rounds dQ to bf16.  head_dim 64: 256 keys as 8 waves x 32 (two
+// waves per SIMD).  head_dim 128: 128 keys as 4 waves x 32 (one wave per
+// SIMD), double-buffered query blocks and dS^T with the previous block's dQ
+// computed after the current block's scores.
 #include "attn64.h"
 
 #include <type_traits>
@@ -27,7 +30,6 @@ namespace {
 
 constexpr int kBlockM = 128;  // forward: queries per workgroup
 constexpr int kBlockN = 64;   // forward: keys per LDS tile
-constexpr int kBwdN = 128;    // backward (head_dim 128): keys per workgroup
 constexpr int kBwd64Threads = 512;  // backward (head_dim 64): 8 waves of 32 keys
 constexpr int kBwd64Keys = 256;     // backward (head_dim 64): keys per workgroup
 constexpr int kBwdM = 64;     // backward: queries per step
@@ -267,232 +269,6 @@ __global__ void attn_bwd_pre_kernel(View O, View dO, float* __restrict__ delta, 
 }
 
 template <int D>
-__global__ void __launch_bounds__(256, 2)
-    attn_bwd_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse, const float* __restrict__ delta,
-                    const int32_t* __restrict__ seg, float* __restrict__ dq_acc, MutView dK, MutView dV, int B, int H,
-                    int S, float scale, float scale_log2) {
-  constexpr int KC = D / 16;
-  constexpr int DB = D / 32;
-  constexpr int QS = D + 8;        // Q / dO row stride
-  constexpr int TS = kBwdM + 4;    // Q^T / dO^T row stride
-  constexpr int SS = kBwdN + 8;    // dS row stride
-  constexpr int KTS = kBwdN + 8;   // K^T row stride
-  __shared__ __attribute__((aligned(16))) bf16 Qs[kBwdM * QS];
-  __shared__ __attribute__((aligned(16))) bf16 dOs[kBwdM * QS];
-  __shared__ __attribute__((aligned(16))) bf16 Qt[D * TS];
-  __shared__ __attribute__((aligned(16))) bf16 dOt[D * TS];
-  __shared__ __attribute__((aligned(16))) bf16 dSs[kBwdM * SS];
-  __shared__ __attribute__((aligned(16))) bf16 Kt[D * KTS];
-  __shared__ float lse_s[kBwdM], delta_s[kBwdM];
-  __shared__ int seg_s[kBwdM];
-
-  const int nkv = (S + kBwdN - 1) / kBwdN;
-  int bh, kb;
-  xcd_map(blockIdx.x, nkv, B * H, bh, kb);
-  const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5, l32 = lane & 31;
-  const int k0 = kb * kBwdN;
-  const int kw0 = k0 + 32 * wave;
-  const int my_k = kw0 + l32;
-  const bool k_ok = my_k < S;
-
-  // The wave's own keys as B operands (N = key = lane%32, k = d).
-  bf16x8 kreg[KC], vreg[KC];
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    if (k_ok) {
-      kreg[kc] = *reinterpret_cast<const bf16x8*>(K.row(b, h, my_k) + 16 * kc + 8 * hl);
-      vreg[kc] = *reinterpret_cast<const bf16x8*>(V.row(b, h, my_k) + 16 * kc + 8 * hl);
-    } else {
-      kreg[kc] = bf16x8{};
-      vreg[kc] = bf16x8{};
-    }
-  }
-  const int seg_k = (seg && k_ok) ? seg[(size_t)b * S + my_k] : 0;
-
-  // K^T of the workgroup's 128 keys for the dQ product.
-  for (int idx = tid; idx < kBwdN * D / 8; idx += 256) {
-    int key = idx / (D / 8), dc = (idx % (D / 8)) * 8;
-    bf16x8 kv = bf16x8{};
-    if (k0 + key < S) kv = *reinterpret_cast<const bf16x8*>(K.row(b, h, k0 + key) + dc);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) Kt[(dc + j) * KTS + key] = kv[j];
-  }
-
-  f32x16 dv_acc[DB], dk_acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    dv_acc[db] = f32x16{};
-    dk_acc[db] = f32x16{};
-  }
-
-  const float* lse_bh = lse + (size_t)bh * S;
-  const float* delta_bh = delta + (size_t)bh * S;
-  float* dq_bh = dq_acc + (size_t)bh * S * D;
-
-  constexpr int kLoads = kBwdM * D / 8 / 256;
-  bf16x8 qst[kLoads], gst[kLoads];
-  float lse_st = 0.f, delta_st = 0.f;
-  int seg_st = 0;
-  auto load_q = [&](int qq0) {
-#pragma unroll
-    for (int r = 0; r < kLoads; ++r) {
-      int idx = tid + 256 * r;
-      int qi = idx / (D / 8), dc = (idx % (D / 8)) * 8;
-      if (qq0 + qi < S) {
-        qst[r] = *reinterpret_cast<const bf16x8*>(Q.row(b, h, qq0 + qi) + dc);
-        gst[r] = *reinterpret_cast<const bf16x8*>(dO.row(b, h, qq0 + qi) + dc);
-      } else {
-        qst[r] = bf16x8{};
-        gst[r] = bf16x8{};
-      }
-    }
-    if (tid < kBwdM) {
-      int q = qq0 + tid;
-      lse_st = q < S ? lse_bh[q] * GPTRIG_LOG2E : 0.f;
-      delta_st = q < S ? delta_bh[q] : 0.f;
-      seg_st = (seg && q < S) ? seg[(size_t)b * S + q] : 0;
-    }
-  };
-  auto store_q = [&]() {
-#pragma unroll
-    for (int r = 0; r < kLoads; ++r) {
-      int idx = tid + 256 * r;
-      int qi = idx / (D / 8), dc = (idx % (D / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(&Qs[qi * QS + dc]) = qst[r];
-      *reinterpret_cast<bf16x8*>(&dOs[qi * QS + dc]) = gst[r];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        Qt[(dc + j) * TS + qi] = qst[r][j];
-        dOt[(dc + j) * TS + qi] = gst[r][j];
-      }
-    }
-    if (tid < kBwdM) {
-      lse_s[tid] = lse_st;
-      delta_s[tid] = delta_st;
-      seg_s[tid] = seg_st;
-    }
-  };
-
-  const int qb_first = k0 / kBwdM;
-  const int nqb = (S + kBwdM - 1) / kBwdM;
-  load_q(qb_first * kBwdM);
-
-  for (int qb = qb_first; qb < nqb; ++qb) {
-    const int qq0 = qb * kBwdM;
-    store_q();
-    __syncthreads();  // (A) Q, dO, transposes, lse, delta published
-    if (qb + 1 < nqb) load_q(qq0 + kBwdM);
-
-    const bool wave_active = kw0 <= qq0 + kBwdM - 1 && kw0 < S;
-    const bool need_mask = (qq0 < kw0 + 31) || (qq0 + kBwdM > S) || (kw0 + 32 > S) || seg;
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      if (!wave_active) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          int qi = 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
-          dSs[qi * SS + 32 * wave + l32] = (bf16)0.f;
-        }
-        continue;
-      }
-      f32x16 sacc = f32x16{}, pacc = f32x16{};
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        bf16x8 aq = *reinterpret_cast<const bf16x8*>(&Qs[(32 * qs + l32) * QS + 16 * kc + 8 * hl]);
-        bf16x8 ag = *reinterpret_cast<const bf16x8*>(&dOs[(32 * qs + l32) * QS + 16 * kc + 8 * hl]);
-        sacc = mfma32(aq, kreg[kc], sacc);
-        pacc = mfma32(ag, vreg[kc], pacc);
-      }
-      bf16x8 pb[2], db8[2];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int qi = 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
-        float p = fast_exp2(sacc[i] * scale_log2 - lse_s[qi]);
-        if (need_mask) {
-          const int q = qq0 + qi;
-          bool vis = my_k <= q && q < S && k_ok;
-          if (seg && vis) vis = seg_s[qi] == seg_k;
-          p = vis ? p : 0.f;
-        }
-        float ds = p * (pacc[i] - delta_s[qi]) * scale;
-        pb[i >> 3][i & 7] = (bf16)p;
-        bf16 dsb = (bf16)ds;
-        db8[i >> 3][i & 7] = dsb;
-        dSs[qi * SS + 32 * wave + l32] = dsb;
-      }
-      // dV^T += dO^T P ; dK^T += Q^T dS   (contraction over this sub-block's 32 queries)
-#pragma unroll
-      for (int dbk = 0; dbk < DB; ++dbk) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int col = 32 * qs + 16 * c + 4 * hl;
-          const bf16* grow = &dOt[(32 * dbk + l32) * TS + col];
-          const bf16* qrow = &Qt[(32 * dbk + l32) * TS + col];
-          bf16x4 glo = *reinterpret_cast<const bf16x4*>(grow);
-          bf16x4 ghi = *reinterpret_cast<const bf16x4*>(grow + 8);
-          bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qrow);
-          bf16x4 qhi = *reinterpret_cast<const bf16x4*>(qrow + 8);
-          bf16x8 ag = {glo[0], glo[1], glo[2], glo[3], ghi[0], ghi[1], ghi[2], ghi[3]};
-          bf16x8 aq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
-          dv_acc[dbk] = mfma32(ag, pb[c], dv_acc[dbk]);
-          dk_acc[dbk] = mfma32(aq, db8[c], dk_acc[dbk]);
-        }
-      }
-    }
-    __syncthreads();  // (B) dS published
-
-    // dQ tile of this wave: queries 32*(wave/2).., d 32*(wave%2).. over all 128 keys.
-    {
-      const int qs = wave >> 1;
-      f32x16 dq_tile[DB / 2 > 0 ? DB / 2 : 1];
-      // For D=64 each wave owns one 32x32 tile; for D=128 two (d blocks wave%2 and wave%2+2).
-#pragma unroll
-      for (int t = 0; t < (DB + 1) / 2; ++t) dq_tile[t] = f32x16{};
-#pragma unroll
-      for (int kc = 0; kc < kBwdN / 16; ++kc) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&dSs[(32 * qs + l32) * SS + 16 * kc + 8 * hl]);
-#pragma unroll
-        for (int t = 0; t < (DB + 1) / 2; ++t) {
-          const int dblk = (wave & 1) + 2 * t;
-          bf16x8 bk = *reinterpret_cast<const bf16x8*>(&Kt[(32 * dblk + l32) * KTS + 16 * kc + 8 * hl]);
-          dq_tile[t] = mfma32(a, bk, dq_tile[t]);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < (DB + 1) / 2; ++t) {
-        const int dcol = 32 * ((wave & 1) + 2 * t) + l32;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int q = qq0 + 32 * qs + 8 * (i >> 2) + 4 * hl + (i & 3);
-          if (q < S) atomicAdd(dq_bh + (size_t)q * D + dcol, dq_tile[t][i]);
-        }
-      }
-    }
-  }
-
-  if (k_ok) {
-    bf16* dvrow = dV.row(b, h, my_k);
-    bf16* dkrow = dK.row(b, h, my_k);
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bf16x4 v4, k4;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          v4[t] = (bf16)dv_acc[db][4 * r + t];
-          k4[t] = (bf16)dk_acc[db][4 * r + t];
-        }
-        *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * r + 4 * hl) = v4;
-        *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * r + 4 * hl) = k4;
-      }
-    }
-  }
-}
-
-template <int D>
 // rcs / rsn (nullable): RoPE tables [S][D/2]; when given, the bf16 dQ is
 // passed back through the transposed rotation (the RoPE VJP) before the store.
 __global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView dQ, int B, int H, int S,
@@ -520,29 +296,6 @@ __global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView
   *reinterpret_cast<bf16x8*>(dQ.row(bh / H, bh % H, s) + 8 * c) = o;
 }
 
-// Transposed RoPE rotation, in place, of a strided [B, H, S, D] bf16 view
-// (dK of the head_dim 128 backward): one thread per 8 values.
-__global__ void rope_view_bwd_kernel(MutView X, int B, int H, int S, int D, const bf16* __restrict__ rcs,
-                                     const bf16* __restrict__ rsn) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int per_row = D / 8;
-  const int64_t row = t / per_row;
-  const int c = (int)(t % per_row);
-  if (row >= (int64_t)B * H * S) return;
-  const int s = (int)(row % S);
-  const int bh = (int)(row / S);
-  bf16* p = X.row(bh / H, bh % H, s) + 8 * c;
-  bf16x8 o = *reinterpret_cast<const bf16x8*>(p);
-  const bf16x4 c4 = *reinterpret_cast<const bf16x4*>(rcs + (size_t)s * (D / 2) + 4 * c);
-  const bf16x4 s4 = *reinterpret_cast<const bf16x4*>(rsn + (size_t)s * (D / 2) + 4 * c);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bf16x2 r = rope_pair((float)o[2 * j], (float)o[2 * j + 1], (float)c4[j], -(float)s4[j]);
-    o[2 * j] = r[0];
-    o[2 * j + 1] = r[1];
-  }
-  *reinterpret_cast<bf16x8*>(p) = o;
-}
 
 
 // ============================================================================
@@ -993,6 +746,344 @@ __global__ void __launch_bounds__(kBwd64Threads, 2)
   }
 }
 
+// ============================================================================
+// Backward, head_dim 128
+// ============================================================================
+// A workgroup owns 128 keys as 4 waves x 32 keys, one wave per SIMD (the dV /
+// dK accumulators of 32 keys x 128 d are 128 registers per wave).  Each wave
+// keeps its keys' K and V operands in registers for the whole loop.  Q / dO /
+// lse / Delta and dS^T are double-buffered, one barrier per query block: a
+// wave computes this block's scores and dV / dK, stores the prefetched next
+// block to LDS, then computes the previous block's dQ tile and adds it with
+// fp32 atomics.  Every 128-wide matrix in LDS is kept as two 64-wide
+// swizzled tiles (d 0..63, then d 64..127), so the head_dim-64 swizzle and
+// its row and transposed reads serve it unchanged.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kBwd128Threads = 256;
+constexpr int kBwd128Keys = 128;
+
+// Element offset of 16-byte chunk c16 (0..15) of row `row` in a 128-wide
+// matrix of `rows` rows stored as two 64-wide tiles.
+__device__ __forceinline__ int at128(int rows, int row, int c16) {
+  return (c16 >> 3) * rows * 64 + at64::swz(row, c16 & 7);
+}
+
+template <bool kSeg>
+__global__ void __launch_bounds__(kBwd128Threads, 1)
+    attn_bwd128_kernel(View Q, View K, View V, View dO, const float* __restrict__ lse,
+                       const float* __restrict__ delta, const int32_t* __restrict__ seg, float* __restrict__ dq_acc,
+                       MutView dK, MutView dV, int B, int H, int S, float scale, float scale_log2,
+                       const bf16* __restrict__ rcs, const bf16* __restrict__ rsn) {
+  constexpr int D = 128, KC = D / 16, DB = D / 32, NT = kBwd128Threads, NK = kBwd128Keys, M = kBwdM;
+  __shared__ __attribute__((aligned(16))) bf16 q_smem[2 * M * D];
+  __shared__ __attribute__((aligned(16))) bf16 g_smem[2 * M * D];
+  __shared__ __attribute__((aligned(16))) bf16 k_smem[NK * D];
+  __shared__ __attribute__((aligned(16))) bf16 ds_smem[2 * NK * M];
+  __shared__ __attribute__((aligned(16))) float lse_s[2 * M], delta_s[2 * M];
+  __shared__ int seg_s[2 * M];
+  at64::lds_t* const Ks = gemm::lds_cast(k_smem);
+
+  const int nkv = (S + NK - 1) / NK;
+  int bh, kb;
+  xcd_map(blockIdx.x, nkv, B * H, bh, kb);
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int k0 = kb * NK;
+  const int kw0 = k0 + 32 * wave;
+  const int my_k = kw0 + l32;
+
+  // The workgroup's K tile (dQ operand) into LDS and this wave's K and V
+  // operands (B operands of S = Q K^T and dP = dO V^T, k = d) into registers,
+  // through buffer resources over the (b, h) slice (rows at or past S read
+  // as zeros); every load is issued before the first wait.
+  const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(K.row(b, h, 0), (uint32_t)(S * K.ss * 2));
+  const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(V.row(b, h, 0), (uint32_t)(S * V.ss * 2));
+  constexpr int KR = NK * (D / 8) / NT;
+  bf16x8 kst[KR];
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    const int idx = tid + NT * r;
+    kst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                            k_rs, ((k0 + (idx >> 4)) * (int)K.ss + 8 * (idx & 15)) * 2, 0, 0));
+  }
+  bf16x8 kfr[KC], vfr[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    kfr[kc] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                             k_rs, (my_k * (int)K.ss + 8 * (2 * kc + hl)) * 2, 0, 0));
+    vfr[kc] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                             v_rs, (my_k * (int)V.ss + 8 * (2 * kc + hl)) * 2, 0, 0));
+  }
+  const int seg_k = (kSeg && my_k < S) ? seg[(size_t)b * S + my_k] : 0;
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    const int idx = tid + NT * r;
+    *(at64::lds_x8*)(Ks + at128(NK, idx >> 4, idx & 15)) = kst[r];
+  }
+
+  f32x16 dv_acc[DB], dk_acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dv_acc[db] = f32x16{};
+    dk_acc[db] = f32x16{};
+  }
+  const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(Q.row(b, h, 0), (uint32_t)(S * Q.ss * 2));
+  const __amdgpu_buffer_rsrc_t g_rs = make_rsrc(dO.row(b, h, 0), (uint32_t)(S * dO.ss * 2));
+  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (size_t)bh * S, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t delta_rs = make_rsrc(delta + (size_t)bh * S, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t seg_rs =
+      make_rsrc(kSeg ? (const void*)(seg + (size_t)b * S) : (const void*)lse, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t dq_rs = make_rsrc(dq_acc + (size_t)bh * S * D, (uint32_t)S * D * 4u);
+
+  // Register staging of one query block: 4 x 16 B of Q and of dO per thread.
+  constexpr int QR = M * (D / 8) / NT;
+  bf16x8 qst[QR], gst[QR];
+  float lse_st = 0.f, delta_st = 0.f;
+  int seg_st = 0;
+  auto load_q = [&](int qq0) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int idx = tid + NT * r;
+      const int qi = idx >> 4, c = idx & 15;
+      qst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              q_rs, ((qq0 + qi) * (int)Q.ss + 8 * c) * 2, 0, 0));
+      gst[r] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              g_rs, ((qq0 + qi) * (int)dO.ss + 8 * c) * 2, 0, 0));
+    }
+    if (tid < M) {
+      lse_st = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lse_rs, (qq0 + tid) * 4, 0, 0));
+      delta_st = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(delta_rs, (qq0 + tid) * 4, 0, 0));
+      if (kSeg) seg_st = (int)__builtin_amdgcn_raw_buffer_load_b32(seg_rs, (qq0 + tid) * 4, 0, 0);
+    }
+  };
+  auto store_q = [&](int buf) {
+    at64::lds_t* const Qs = gemm::lds_cast(q_smem) + buf * M * D;
+    at64::lds_t* const dOs = gemm::lds_cast(g_smem) + buf * M * D;
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int idx = tid + NT * r;
+      *(at64::lds_x8*)(Qs + at128(M, idx >> 4, idx & 15)) = qst[r];
+      *(at64::lds_x8*)(dOs + at128(M, idx >> 4, idx & 15)) = gst[r];
+    }
+    if (tid < M) {
+      lse_s[buf * M + tid] = lse_st * GPTRIG_LOG2E;
+      delta_s[buf * M + tid] = delta_st * scale;  // dS = P * (scale*dP - scale*Delta)
+      if (kSeg) seg_s[buf * M + tid] = seg_st;
+    }
+  };
+
+  // dQ of a query block for queries 32*(wave/2).. and d 64*(wave%2).. (two
+  // 32-wide tiles) over all NK keys, from that block's dS^T buffer (a wave
+  // whose keys cannot see the block leaves zeros there), in groups of 32
+  // keys whose LDS reads are issued one group ahead of their MFMAs.
+  auto dq_step = [&](int qq0, int buf) {
+    const at64::lds_t* const dSt = gemm::lds_cast(ds_smem) + buf * NK * M;
+    const at64::lds_t* const Kh = Ks + (wave & 1) * NK * 64;
+    const int qs = wave >> 1;
+    bf16x8 fa[2][2], fb[2][2][2];
+    auto rd = [&](int g) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        fa[g & 1][u] = at64::trfrag<false>(dSt, 32 * qs, 16 * (2 * g + u), lane);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fb[g & 1][u][j] = at64::trfrag<false>(Kh, 32 * j, 16 * (2 * g + u), lane);
+      }
+    };
+    f32x16 acc[2] = {f32x16{}, f32x16{}};
+    rd(0);
+#pragma unroll
+    for (int g = 0; g < NK / 32; ++g) {
+      if (g + 1 < NK / 32) rd(g + 1);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j] = mfma32(fa[g & 1][u], fb[g & 1][u][j], acc[j]);
+    }
+    // Row q = qq0 + 32qs + 4hl + 8(i/4) + i%4 of this lane's column; rows at
+    // or past S fall outside the buffer resource and are dropped.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int voff = ((qq0 + 32 * qs + 4 * hl) * D + 64 * (wave & 1) + 32 * j + l32) * 4;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(acc[j][i], dq_rs, voff + (8 * (i >> 2) + (i & 3)) * D * 4,
+                                                        0, 0);
+    }
+  };
+  // A wave whose keys cannot see a block leaves zeros as its dS^T rows.
+  auto zero_ds = [&](int buf) {
+    at64::lds_t* const dSt = gemm::lds_cast(ds_smem) + buf * NK * M;
+#pragma unroll
+    for (int r = 0; r < 32 * M / 8 / 64; ++r)
+      *(at64::lds_x8*)(dSt + 32 * M * wave + 8 * (lane + 64 * r)) = bf16x8{};
+  };
+
+  const int qb_first = k0 / M;
+  const int nqb = (S + M - 1) / M;
+  load_q(qb_first * M);
+  store_q(0);
+
+  auto begin = [&](int qb) {
+    // Q / dO / lse / Delta of this block and the previous block's dS^T published.
+    GPTRIG_WAIT_LGKM0();
+    wg_barrier();
+    load_q(qb + 1 < nqb ? (qb + 1) * M : qb * M);
+  };
+  auto nbuf = [&](int qb) { return ((qb - qb_first) & 1) ^ 1; };  // the buffer of block qb - 1 / qb + 1
+
+  // Scores, dS and dV / dK of query block qb against this wave's 32 keys.
+  auto body = [&](int qb, auto mask_tag) {
+    constexpr bool kMask = decltype(mask_tag)::value;
+    const int qq0 = qb * M, buf = (qb - qb_first) & 1;
+    const at64::lds_t* const Qs = gemm::lds_cast(q_smem) + buf * M * D;
+    const at64::lds_t* const dOs = gemm::lds_cast(g_smem) + buf * M * D;
+    at64::lds_t* const dSt = gemm::lds_cast(ds_smem) + buf * NK * M;
+    const float* const ls = lse_s + buf * M;
+    const float* const dls = delta_s + buf * M;
+    const int* const sgs = seg_s + buf * M;
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      bf16x8 qf[KC], gf[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        qf[kc] = *(const at64::lds_x8*)(Qs + at128(M, 32 * qs + l32, 2 * kc + hl));
+        gf[kc] = *(const at64::lds_x8*)(dOs + at128(M, 32 * qs + l32, 2 * kc + hl));
+      }
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        sacc = mfma32(qf[kc], kfr[kc], sacc);
+        pacc = mfma32(gf[kc], vfr[kc], pacc);
+      }
+      bf16x8 pb[2], db8[2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qr = 32 * qs + 8 * r + 4 * hl;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&ls[qr]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dls[qr]);
+        bf16x4 ds4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int i = 4 * r + t;
+          float p = fast_exp2(fmaf(sacc[i], scale_log2, -l4[t]));
+          if (kMask) {
+            // Causal; with segment ids also the document.  Queries and keys
+            // at or past S need no mask: their Q / K / dO / V rows, lse and
+            // Delta read as zeros, so they add nothing to dV, dK or dQ.
+            const int q = qq0 + qr + t;
+            bool vis = my_k <= q;
+            if (kSeg && vis) vis = sgs[qr + t] == seg_k;
+            p = vis ? p : 0.f;
+          }
+          const float ds = p * fmaf(pacc[i], scale, -d4[t]);
+          pb[i >> 3][i & 7] = (bf16)p;
+          const bf16 dsb = (bf16)ds;
+          db8[i >> 3][i & 7] = dsb;
+          ds4[t] = dsb;
+        }
+        // dS^T row = this lane's key, queries 32qs + 8r + 4hl .. +3.
+        *(__attribute__((address_space(3))) bf16x4*)(dSt + at64::swz(32 * wave + l32, 4 * qs + r) + 4 * hl) = ds4;
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int half = (db >> 1) * M * 64;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const bf16x8 gt = at64::trfrag<true>(dOs + half, 32 * (db & 1), 32 * qs + 16 * c, lane);
+          const bf16x8 qt = at64::trfrag<true>(Qs + half, 32 * (db & 1), 32 * qs + 16 * c, lane);
+          dv_acc[db] = mfma32(gt, pb[c], dv_acc[db]);
+          dk_acc[db] = mfma32(qt, db8[c], dk_acc[db]);
+        }
+      }
+    }
+  };
+
+  // Per wave: the first block (no dQ before it), the blocks before this
+  // wave's keys (no scores), the diagonal block (causal mask), the blocks
+  // after it (mask-free unless segment ids are given).  Every wave runs
+  // nqb - qb_first blocks, one barrier each, so the barriers match; no dQ is
+  // conditional inside a phase, so the waits for the prefetched block count
+  // the atomics issued after it instead of draining them.
+  const int my_first = min(kw0 / M, nqb);
+  begin(qb_first);
+  if (my_first == qb_first)
+    body(qb_first, std::true_type{});
+  else
+    zero_ds(0);
+  store_q(1);
+  int qb = qb_first + 1;
+  for (; qb < my_first; ++qb) {
+    begin(qb);
+    zero_ds(nbuf(qb) ^ 1);
+    dq_step((qb - 1) * M, nbuf(qb));
+    store_q(nbuf(qb));
+  }
+  if (qb == my_first && qb < nqb) {
+    begin(qb);
+    body(qb, std::true_type{});
+    store_q(nbuf(qb));
+    dq_step((qb - 1) * M, nbuf(qb));
+    ++qb;
+  }
+  for (; qb < nqb; ++qb) {
+    begin(qb);
+    body(qb, std::integral_constant<bool, kSeg>{});
+    store_q(nbuf(qb));
+    dq_step((qb - 1) * M, nbuf(qb));
+  }
+
+  // dV and dK rows of this wave's keys (lane: key my_k, d = 32db + 8r + 4hl
+  // .. +3), with the RoPE VJP of dK when tables are given.  Stores and table
+  // reads go through buffer resources (keys at or past S dropped / read as
+  // zeros); all table reads are issued before the first use.
+  const __amdgpu_buffer_rsrc_t dv_rs = make_rsrc(dV.row(b, h, 0), (uint32_t)(S * dV.ss * 2));
+  const __amdgpu_buffer_rsrc_t dk_rs = make_rsrc(dK.row(b, h, 0), (uint32_t)(S * dK.ss * 2));
+  uint32_t rc[DB][4], rsv[DB][4];
+  if (rcs) {
+    const __amdgpu_buffer_rsrc_t rc_rs = make_rsrc(rcs, (uint32_t)(S * (D / 2) * 2));
+    const __amdgpu_buffer_rsrc_t rs_rs = make_rsrc(rsn, (uint32_t)(S * (D / 2) * 2));
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int off = (my_k * (D / 2) + (32 * db + 8 * r + 4 * hl) / 2) * 2;
+        rc[db][r] = __builtin_amdgcn_raw_buffer_load_b32(rc_rs, off, 0, 0);
+        rsv[db][r] = __builtin_amdgcn_raw_buffer_load_b32(rs_rs, off, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      bf16x4 v4, k4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v4[t] = (bf16)dv_acc[db][4 * r + t];
+        k4[t] = (bf16)dk_acc[db][4 * r + t];
+      }
+      if (rcs) {  // RoPE VJP: pairs (t, t+1) for t = 0, 2
+        const bf16x2 c2 = __builtin_bit_cast(bf16x2, rc[db][r]);
+        const bf16x2 s2 = __builtin_bit_cast(bf16x2, rsv[db][r]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16x2 rr = rope_pair((float)k4[2 * u], (float)k4[2 * u + 1], (float)c2[u], -(float)s2[u]);
+          k4[2 * u] = rr[0];
+          k4[2 * u + 1] = rr[1];
+        }
+      }
+      const int d0 = 32 * db + 8 * r + 4 * hl;
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v4), dv_rs, (my_k * (int)dV.ss + d0) * 2, 0,
+                                            0);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, k4), dk_rs, (my_k * (int)dK.ss + d0) * 2, 0,
+                                            0);
+    }
+  // The last block's dQ, after the dK / dV stores so no store waits for its atomics.
+  GPTRIG_WAIT_LGKM0();
+  wg_barrier();
+  dq_step((nqb - 1) * M, (nqb - 1 - qb_first) & 1);
+}
+
 bool strides_ok(const int64_t* st, int n) {
   // Row starts must stay 16-byte aligned for the vector loads.
   for (int i = 0; i < 3 * n; ++i)
@@ -1085,8 +1176,6 @@ int attn_bwd_impl(const void* q, const void* k, const void* v, const void* o, co
   float* delta = (float*)workspace;
   float* dq_acc = (float*)((char*)workspace + ((rows * sizeof(float) + 255) & ~(size_t)255));
   hipStream_t s = (hipStream_t)stream;
-  const int nkv = (seq + kBwdN - 1) / kBwdN;
-  const long long grid = (long long)batch * heads * nkv;
   const float sl2 = softmax_scale * GPTRIG_LOG2E;
   if (head_dim == 64) {
     // The kernel addresses one (b, h) slice of Q / dO / dq_acc through 32-bit
@@ -1107,19 +1196,24 @@ int attn_bwd_impl(const void* q, const void* k, const void* v, const void* o, co
     attn_dq_convert_kernel<64><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq,
                                                                                    rcs, rsn);
   } else {
-    attn_bwd_pre_kernel<128><<<ceil_div((long long)rows * 8, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
+    const long long span = (long long)seq * (Q.ss > dO.ss ? Q.ss : dO.ss) * 2;
+    const long long kspan = (long long)seq * (K.ss > V.ss ? K.ss : V.ss) * 2;
+    const long long ospan = (long long)seq * (dK.ss > dV.ss ? dK.ss : dV.ss) * 2;
+    if (span >= (1ll << 31) || kspan >= (1ll << 31) || ospan >= (1ll << 31) || (long long)seq * 128 * 4 >= (1ll << 31))
+      return GPTRIG_E_SHAPE;
+    attn_bwd_pre_kernel<128><<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(O, dO, delta, dq_acc, batch, heads,
                                                                                  seq);
     GPTRIG_CHECK_LAUNCH();
-    attn_bwd_kernel<128><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK, dV, batch,
-                                                        heads, seq, softmax_scale, sl2);
+    const unsigned grid128 = (unsigned)((long long)batch * heads * ceil_div(seq, kBwd128Keys));
+    if (segment_ids)
+      attn_bwd128_kernel<true><<<grid128, kBwd128Threads, 0, s>>>(Q, K, V, dO, lse, delta, segment_ids, dq_acc, dK,
+                                                                  dV, batch, heads, seq, softmax_scale, sl2, rcs, rsn);
+    else
+      attn_bwd128_kernel<false><<<grid128, kBwd128Threads, 0, s>>>(Q, K, V, dO, lse, delta, nullptr, dq_acc, dK, dV,
+                                                                   batch, heads, seq, softmax_scale, sl2, rcs, rsn);
     GPTRIG_CHECK_LAUNCH();
     attn_dq_convert_kernel<128><<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(dq_acc, dQ, batch, heads, seq,
                                                                                     rcs, rsn);
-    if (rcs) {
-      GPTRIG_CHECK_LAUNCH();
-      rope_view_bwd_kernel<<<ceil_div((long long)rows * 16, 256), 256, 0, s>>>(dK, batch, heads, seq, head_dim, rcs,
-                                                                               rsn);
-    }
   }
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;

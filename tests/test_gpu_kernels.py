@@ -44,6 +44,9 @@ ATTN_CASES = [
     (2, 2, 129, 64, None, False),       # S = 129 (reference padding test shape)
     (1, 2, 256, 128, None, False),
     (1, 2, 256, 64, None, True),        # document masking
+    (2, 2, 200, 128, None, False),      # head_dim 128, ragged S
+    (1, 2, 320, 128, None, True),       # head_dim 128, document masking
+    (1, 2, 1000, 128, 1.0 / 128, False),  # head_dim 128, ragged S over 8 key blocks
 ]
 
 
@@ -398,7 +401,7 @@ def test_bias_passes_round_the_linear_bias_add_like_the_reference():
     assert torch.equal(s, s2) and torch.equal(yn, yn2) and torch.equal(r, r2)
 
 
-@pytest.mark.parametrize("D,segmented", [(64, False), (64, True), (128, False)])
+@pytest.mark.parametrize("D,segmented", [(64, False), (64, True), (128, False), (128, True)])
 def test_attention_backward_with_rope_vjp_equals_two_passes(D, segmented):
     """gptrig_attn_bwd_rope == gptrig_attn_bwd followed by gptrig_rope_bwd on
     dq and dk, bit for bit, on the training step's interleaved qkv layout; and
