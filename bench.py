@@ -156,6 +156,18 @@ def isolated_configs(reps: int = 20) -> dict:
     fwd_tf = 4 * B * H * D * visible / (fwd_ms / 1e3) / 1e12
     bwd_tf = attn_bwd_flops(B, H, S, D) / (bwd_ms / 1e3) / 1e12
     del q, k, v, do, o, lse
+    # head_dim 128 at the same model width (6 heads x 128; no BASELINE config
+    # uses it): the kernels the reference's D <= 128 range reaches.
+    H2, D2 = 6, 128
+    q, k, v, do = (torch.from_numpy(rng.standard_normal((B, H2, S, D2), dtype=np.float32)).to(dev).bfloat16()
+                   for _ in range(4))
+    sc2 = D2 ** -0.5
+    o, lse = fa.flash_forward(q, k, v, None, sc2)
+    fwd128_ms = timed(lambda: fa.flash_forward(q, k, v, None, sc2))
+    bwd128_ms = timed(lambda: fa.flash_backward(q, k, v, o, lse, do, None, sc2))
+    fwd128_tf = 4 * B * H2 * D2 * visible / (fwd128_ms / 1e3) / 1e12
+    bwd128_tf = attn_bwd_flops(B, H2, S, D2) / (bwd128_ms / 1e3) / 1e12
+    del q, k, v, do, o, lse
 
     n, d, vocab = 16384, 768, 50304
     h = torch.from_numpy(rng.standard_normal((n, d), dtype=np.float32)).to(dev).bfloat16()
@@ -205,6 +217,10 @@ def isolated_configs(reps: int = 20) -> dict:
             "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(fwd_tf, 1), "fwd_frac": round(fwd_tf / peak, 4),
             "bwd_ms": round(bwd_ms, 4), "bwd_tflops": round(bwd_tf, 1), "bwd_frac": round(bwd_tf / peak, 4),
             "bwd_algorithmic_flops": attn_bwd_flops(B, H, S, D)},
+        "attention_B16_H6_S1024_D128": {
+            "fwd_ms": round(fwd128_ms, 4), "fwd_tflops": round(fwd128_tf, 1),
+            "fwd_frac": round(fwd128_tf / peak, 4), "bwd_ms": round(bwd128_ms, 4),
+            "bwd_tflops": round(bwd128_tf, 1), "bwd_frac": round(bwd128_tf / peak, 4)},
         "flce_N16384_d768_V50304": {"ms": round(flce_ms, 4), "tflops": round(flce_tf, 1),
                                     "frac": round(flce_tf / peak, 4), "algorithmic_flops": flce_flops(n, d, vocab),
                                     "path": f"kept softmax over token chunks of {chunk} (the trainer's default: "
