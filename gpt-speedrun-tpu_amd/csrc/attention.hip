@@ -60,185 +60,9 @@ __device__ __forceinline__ void xcd_map(int id, int nblocks, int bh_total, int& 
 }
 
 // ============================================================================
-// Forward
+// Backward passes around the main kernels: Delta (and the dQ accumulator
+// zeroed) before, the dQ conversion to bf16 after
 // ============================================================================
-template <int D>
-__global__ void __launch_bounds__(256, 2)
-    attn_fwd_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
-                    int B, int H, int S, float scale_log2) {
-  constexpr int KS = D + 8;        // K tile row stride (elements)
-  constexpr int VS = kBlockN + 4;  // V^T tile row stride
-  constexpr int KC = D / 16;       // 16-wide k-chunks over head_dim
-  constexpr int DB = D / 32;       // 32-wide d blocks of the output
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][kBlockN * KS];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * VS];
-
-  const int nq = (S + kBlockM - 1) / kBlockM;
-  int bh, qb;
-  xcd_map(blockIdx.x, nq, B * H, bh, qb);
-  qb = nq - 1 - qb;  // heaviest (longest causal prefix) first
-  const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform mask branches
-  const int hl = lane >> 5, l32 = lane & 31;
-  const int q0 = qb * kBlockM;
-  const int qw0 = q0 + wave * 32;
-  const int my_q = qw0 + l32;
-  const int last_q = min(q0 + kBlockM, S) - 1;
-  const int ntiles = last_q / kBlockN + 1;
-
-  // Q^T operand: lane holds query my_q, d = 16kc + 8hl + j.
-  bf16x8 qreg[KC];
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    if (my_q < S)
-      qreg[kc] = *reinterpret_cast<const bf16x8*>(Q.row(b, h, my_q) + 16 * kc + 8 * hl);
-    else
-      qreg[kc] = bf16x8{};
-  }
-  const int seg_q = (seg && my_q < S) ? seg[(size_t)b * S + my_q] : 0;
-
-  f32x16 acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
-  float m_run = kMinusBig, l_run = 0.f;
-
-  // Global -> register staging of one K/V tile: 64 keys x D, 16 B per load.
-  constexpr int kLoads = kBlockN * D / 8 / 256;  // 16-byte chunks per thread
-  bf16x8 kst[kLoads], vst[kLoads];
-  auto load_tile = [&](int kv0) {
-#pragma unroll
-    for (int r = 0; r < kLoads; ++r) {
-      int idx = tid + 256 * r;
-      int key = idx / (D / 8), dc = (idx % (D / 8)) * 8;
-      if (kv0 + key < S) {
-        kst[r] = *reinterpret_cast<const bf16x8*>(K.row(b, h, kv0 + key) + dc);
-        vst[r] = *reinterpret_cast<const bf16x8*>(V.row(b, h, kv0 + key) + dc);
-      } else {
-        kst[r] = bf16x8{};
-        vst[r] = bf16x8{};
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < kLoads; ++r) {
-      int idx = tid + 256 * r;
-      int key = idx / (D / 8), dc = (idx % (D / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(&Ks[buf][key * KS + dc]) = kst[r];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[buf][(dc + j) * VS + key] = vst[r][j];
-    }
-  };
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int kv0 = it * kBlockN;
-    if (it + 1 < ntiles) load_tile(kv0 + kBlockN);
-
-    if (kv0 <= qw0 + 31) {  // some key of this tile is visible to this wave
-      f32x16 s[2];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        s[sb] = f32x16{};
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[buf][(32 * sb + l32) * KS + 16 * kc + 8 * hl]);
-          s[sb] = mfma32(a, qreg[kc], s[sb]);
-        }
-      }
-      // One uniform branch per tile (the diagonal, ragged and segmented tiles).
-      if ((kv0 + kBlockN - 1 > qw0) || (kv0 + kBlockN > S) || seg) {
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kv0 + 32 * sb + 8 * (i >> 2) + 4 * hl + (i & 3);
-            bool vis = key <= my_q && key < S;
-            if (seg && vis) vis = seg[(size_t)b * S + key] == seg_q;
-            s[sb][i] = vis ? s[sb][i] : -INFINITY;
-          }
-      }
-      float mloc = kMinusBig;
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float x = s[sb][i] * scale_log2;
-          s[sb][i] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float m_new = fmaxf(m_run, mloc);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      float lsum = 0.f;
-      bf16x8 pb[4];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            float p = fast_exp2(s[sb][8 * c2 + j] - m_new);
-            lsum += p;
-            pb[2 * sb + c2][j] = (bf16)p;
-          }
-        }
-      }
-      l_run = l_run * alpha + lsum;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-      }
-      // O^T += V^T P^T over the tile's 4 key chunks of 16.
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bf16* row = &Vt[buf][(32 * db + l32) * VS + 16 * c + 4 * hl];
-          bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
-          bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8);
-          bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          acc[db] = mfma32(a, pb[c], acc[db]);
-        }
-      }
-    }
-
-    if (it + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (my_q < S) {
-    const float inv = 1.0f / l_tot;
-    bf16* orow = O.row(b, h, my_q);
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bf16x4 o4;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) o4[t] = (bf16)(acc[db][4 * r + t] * inv);
-        *reinterpret_cast<bf16x4*>(orow + 32 * db + 8 * r + 4 * hl) = o4;
-      }
-    }
-    if (hl == 0) lse[((size_t)b * H + h) * S + my_q] = (m_run + __log2f(l_tot)) * GPTRIG_LN2;
-  }
-}
-
-// ============================================================================
-// Backward
-// ============================================================================
-
-// Delta = rowsum(float(O) * float(dO)) (tpu_flash_attention.py:532-535) and a
-// zeroed fp32 dQ accumulator.  8 lanes per row.
 template <int D>
 __global__ void attn_bwd_pre_kernel(View O, View dO, float* __restrict__ delta, float* __restrict__ dq_acc, int B,
                                     int H, int S) {
@@ -296,36 +120,33 @@ __global__ void attn_dq_convert_kernel(const float* __restrict__ dq_acc, MutView
   *reinterpret_cast<bf16x8*>(dQ.row(bh / H, bh % H, s) + 8 * c) = o;
 }
 
-
-
 // ============================================================================
-// head_dim 64 kernels on swizzled row-major LDS tiles (attn64.h)
+// Kernels on swizzled row-major LDS tiles (attn64.h)
 // ============================================================================
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Forward: K/V tiles of 64 keys are copied global -> LDS by the DMA path
-// (buffer_load_dwordx4 ... lds) into double-buffered swizzled tiles, one LDS array
-// per buffer and operand so the compiler can see that the copy into one
-// buffer never aliases reads of the other; V^T operands come from transposed
-// reads with the accumulator's row order.  A tile is consumed in two halves
-// of 32 keys (online softmax per half), which keeps the wave under 128 VGPRs:
-// four waves per SIMD hide the LDS and exp latencies.
-__shared__ __attribute__((aligned(16))) bf16 g_fk0[64 * 64];
-__shared__ __attribute__((aligned(16))) bf16 g_fk1[64 * 64];
-__shared__ __attribute__((aligned(16))) bf16 g_fv0[64 * 64];
-__shared__ __attribute__((aligned(16))) bf16 g_fv1[64 * 64];
-
-template <int BUF>
-__device__ __forceinline__ at64::lds_t* fwd_k() { return gemm::lds_cast(BUF ? g_fk1 : g_fk0); }
-template <int BUF>
-__device__ __forceinline__ at64::lds_t* fwd_v() { return gemm::lds_cast(BUF ? g_fv1 : g_fv0); }
-
-template <bool kSeg>
-__global__ void __launch_bounds__(256, 4)
-    attn_fwd64_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
-                      int B, int H, int S, float scale_log2) {
-  constexpr int D = 64, KC = 4, DB = 2;
+// Forward (head_dim 64 and 128): K/V tiles of 64 keys are copied global ->
+// LDS by the DMA path (buffer_load_dwordx4 ... lds) into double-buffered
+// swizzled tiles, one LDS array per buffer and operand so the compiler can see
+// that the copy into one buffer never aliases reads of the other; V^T
+// operands come from transposed reads with the accumulator's row order.  A
+// head_dim-128 tile is kept as two 64-wide swizzled tiles (d 0..63, then d
+// 64..127) so the same swizzle and reads serve it.  A tile is consumed in two
+// halves of 32 keys (online softmax per half): at head_dim 64 that keeps the
+// wave under 128 VGPRs (four waves per SIMD hide the LDS and exp latencies),
+// at head_dim 128 (twice the O accumulator and Q operands) two workgroups
+// share a CU.
+template <int D, bool kSeg>
+__device__ __forceinline__ void attn_fwd_swz(View Q, View K, View V, MutView O, float* __restrict__ lse,
+                                             const int32_t* __restrict__ seg, int B, int H, int S, float scale_log2) {
+  constexpr int KC = D / 16, DB = D / 32;
+  // Element offset of 16-byte chunk c16 of tile row `row` (64 rows per tile).
+  auto tofs = [](int row, int c16) { return (c16 >> 3) * 64 * 64 + at64::swz(row, c16 & 7); };
+  __shared__ __attribute__((aligned(16))) bf16 fk0[64 * D];
+  __shared__ __attribute__((aligned(16))) bf16 fk1[64 * D];
+  __shared__ __attribute__((aligned(16))) bf16 fv0[64 * D];
+  __shared__ __attribute__((aligned(16))) bf16 fv1[64 * D];
 
   const int nq = (S + kBlockM - 1) / kBlockM;
   int bh, qb;
@@ -358,20 +179,24 @@ __global__ void __launch_bounds__(256, 4)
   // rows at or past S read as zeros.
   const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(K.row(b, h, 0), (uint32_t)(S * K.ss * 2));
   const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(V.row(b, h, 0), (uint32_t)(S * V.ss * 2));
+  // Wave w fills 1 KB blocks NBW*w .. NBW*w + NBW-1 of each tile: block blk
+  // holds rows 8*(blk % 8) .. +7 of the 64-wide tile blk / 8.
+  constexpr int NBW = D / 32;
   const int kss2 = (int)K.ss * 2, vss2 = (int)V.ss * 2;
-  int koff[2], voff[2];
+  int koff[NBW], voff[NBW];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = 8 * (2 * wave + j) + (lane >> 3);
+  for (int j = 0; j < NBW; ++j) {
+    const int blk = NBW * wave + j;
+    const int row = 8 * (blk & 7) + (lane >> 3);
     const int t = (row >> 1) & 7;
-    const int c = (lane & 7) ^ (((t & 1) << 2) | (t >> 1));
+    const int c = 8 * (blk >> 3) + ((lane & 7) ^ (((t & 1) << 2) | (t >> 1)));
     koff[j] = row * kss2 + 16 * c;
     voff[j] = row * vss2 + 16 * c;
   }
   auto fill = [&](at64::lds_t* kt, at64::lds_t* vt, int kv0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int blk = 2 * wave + j;
+    for (int j = 0; j < NBW; ++j) {
+      const int blk = NBW * wave + j;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, (lds_void*)(kt + blk * 512), 16, koff[j] + kv0 * kss2, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rs, (lds_void*)(vt + blk * 512), 16, voff[j] + kv0 * vss2, 0, 0, 0);
     }
@@ -381,7 +206,8 @@ __global__ void __launch_bounds__(256, 4)
   auto half = [&](const at64::lds_t* kt, const at64::lds_t* vt, int kv0, int sb) __attribute__((always_inline)) {
     f32x16 s = f32x16{};
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) s = mfma32(at64::rowfrag(kt, 32 * sb + l32, 2 * kc + hl), qreg[kc], s);
+    for (int kc = 0; kc < KC; ++kc)
+      s = mfma32(*(const at64::lds_x8*)(kt + tofs(32 * sb + l32, 2 * kc + hl)), qreg[kc], s);
     // Row max on raw scores (scale > 0); masked scores become -inf.
     const int kh0 = kv0 + 32 * sb;
     float mraw = -INFINITY;
@@ -437,7 +263,8 @@ __global__ void __launch_bounds__(256, 4)
     for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
       for (int db = 0; db < DB; ++db)
-        acc[db] = mfma32(at64::trfrag<true>(vt, 32 * db, 16 * (2 * sb + c2), lane), pb[c2], acc[db]);
+        acc[db] = mfma32(at64::trfrag<true>(vt + (db >> 1) * 64 * 64, 32 * (db & 1), 16 * (2 * sb + c2), lane),
+                         pb[c2], acc[db]);
   };
 
   auto tile = [&](const at64::lds_t* kt, const at64::lds_t* vt, at64::lds_t* nkt, at64::lds_t* nvt, int it) {
@@ -451,12 +278,16 @@ __global__ void __launch_bounds__(256, 4)
     __syncthreads();
   };
 
-  fill(fwd_k<0>(), fwd_v<0>(), 0);
+  at64::lds_t* const k0s = gemm::lds_cast(fk0);
+  at64::lds_t* const k1s = gemm::lds_cast(fk1);
+  at64::lds_t* const v0s = gemm::lds_cast(fv0);
+  at64::lds_t* const v1s = gemm::lds_cast(fv1);
+  fill(k0s, v0s, 0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   for (int it = 0; it < ntiles; it += 2) {
-    tile(fwd_k<0>(), fwd_v<0>(), fwd_k<1>(), fwd_v<1>(), it);
-    if (it + 1 < ntiles) tile(fwd_k<1>(), fwd_v<1>(), fwd_k<0>(), fwd_v<0>(), it + 1);
+    tile(k0s, v0s, k1s, v1s, it);
+    if (it + 1 < ntiles) tile(k1s, v1s, k0s, v0s, it + 1);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -474,6 +305,20 @@ __global__ void __launch_bounds__(256, 4)
       }
     if (hl == 0) lse[((size_t)b * H + h) * S + my_q] = (m_run + __log2f(l_tot)) * GPTRIG_LN2;
   }
+}
+
+template <bool kSeg>
+__global__ void __launch_bounds__(256, 4)
+    attn_fwd64_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
+                      int B, int H, int S, float scale_log2) {
+  attn_fwd_swz<64, kSeg>(Q, K, V, O, lse, seg, B, H, S, scale_log2);
+}
+
+template <bool kSeg>
+__global__ void __launch_bounds__(256, 2)
+    attn_fwd128_kernel(View Q, View K, View V, MutView O, float* __restrict__ lse, const int32_t* __restrict__ seg,
+                       int B, int H, int S, float scale_log2) {
+  attn_fwd_swz<128, kSeg>(Q, K, V, O, lse, seg, B, H, S, scale_log2);
 }
 
 // Backward: KV-owned, 256 keys per workgroup (32 per wave), 64 queries per
@@ -1124,17 +969,19 @@ int gptrig_attn_fwd(const void* q, const void* k, const void* v, const int32_t* 
   const long long grid = (long long)batch * heads * nq;
   const float sl2 = softmax_scale * GPTRIG_LOG2E;
   hipStream_t s = (hipStream_t)stream;
-  if (head_dim == 64)
-  {
-    // The kernel copies one (b, h) slice of K / V through 32-bit buffer offsets.
-    if ((long long)seq * (K.ss > V.ss ? K.ss : V.ss) * 2 >= (1ll << 31)) return GPTRIG_E_SHAPE;
+  // The kernels copy one (b, h) slice of K / V through 32-bit buffer offsets.
+  if ((long long)seq * (K.ss > V.ss ? K.ss : V.ss) * 2 >= (1ll << 31)) return GPTRIG_E_SHAPE;
+  if (head_dim == 64) {
     if (segment_ids)
       attn_fwd64_kernel<true><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
     else
       attn_fwd64_kernel<false><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, nullptr, batch, heads, seq, sl2);
+  } else {
+    if (segment_ids)
+      attn_fwd128_kernel<true><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
+    else
+      attn_fwd128_kernel<false><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, nullptr, batch, heads, seq, sl2);
   }
-  else
-    attn_fwd_kernel<128><<<(unsigned)grid, 256, 0, s>>>(Q, K, V, O, lse, segment_ids, batch, heads, seq, sl2);
   GPTRIG_CHECK_LAUNCH();
   return GPTRIG_OK;
 }
