@@ -47,6 +47,8 @@ ATTN_CASES = [
     (2, 2, 200, 128, None, False),      # head_dim 128, ragged S
     (1, 2, 320, 128, None, True),       # head_dim 128, document masking
     (1, 2, 1000, 128, 1.0 / 128, False),  # head_dim 128, ragged S over 8 key blocks
+    (1, 2, 1, 128, None, False),        # head_dim 128, single position
+    (2, 1, 65, 128, None, False),       # head_dim 128, one key block, two query blocks
 ]
 
 
@@ -145,14 +147,26 @@ def test_attention_autograd_api_and_strided_inputs():
         assert maxabs(grads[:, :, i].permute(0, 2, 1, 3), want) <= 2e-2
 
 
-def test_attention_small_head_dim_is_padded():
+@pytest.mark.parametrize("D", [8, 96])
+def test_attention_small_head_dim_is_padded(D):
+    """head_dim 8 runs padded to 64, head_dim 96 padded to 128 (forward and,
+    through autograd, backward), against the oracle at the true head_dim."""
     from gptrig.kernels import AttentionConfig, make_causal_attention
 
-    q, k, v = (randn((1, 2, 96, 8), s, 0.15) for s in (21, 22, 23))
-    want = oattn.reference_causal_attention(q, k, v)
-    got = make_causal_attention(AttentionConfig())(q.to(DEV), k.to(DEV), v.to(DEV))
+    q, k, v = (randn((1, 2, 96, D), s, 0.15) for s in (21, 22, 23))
+    do = randn((1, 2, 96, D), 24)
+    qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+    want = oattn.reference_causal_attention(qr, kr, vr)
+    want.backward(do.float())
+    qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    got = make_causal_attention(AttentionConfig())(qg, kg, vg)
+    got.backward(do.to(DEV))
+    torch.cuda.synchronize()
     assert got.shape == want.shape
     assert maxabs(got, want) <= 2e-2
+    for g_got, g_want in ((qg.grad, qr.grad), (kg.grad, kr.grad), (vg.grad, vr.grad)):
+        assert g_got.shape == g_want.shape
+        assert maxabs(g_got, g_want) <= 2e-2
 
 
 def test_attention_full_config_b_slice_matches_oracle():
