@@ -110,6 +110,39 @@ def test_train_step_flce_paths_match_oracle(label, model, trainer_only):
     assert abs(ratio - 1) <= 0.1 and cos >= 0.9
 
 
+def test_train_step_head_dim_128_matches_oracle():
+    """A 2-layer model with 2 heads of 128 (d_model 256): the trainer's
+    attention runs the head_dim-128 kernels on the interleaved qkv rows, with
+    the RoPE VJP fused into the backward; history against the oracle's step."""
+    from gptrig.optim import OptimizerConfig
+    from gptrig.train import GPTConfig, GPTTrainer
+
+    steps = 3
+    common = dict(layers=2, heads=2, d_model=256, vocab_size=1000, semantic_vocab_size=997, seq_len=128,
+                  batch_size=4, base_width=256, base_depth=2, attention_scale="inverse_sqrt_head_dim",
+                  embeddings="untied")
+    opt = dict(learning_rate=2.0 ** -8, steps=steps, warmup_steps=1)
+    ocfg = om.Config(**common, attention_backend="flash", optimizer=oopt.OptimizerConfig(**opt))
+    gcfg = GPTConfig(**common, micro_batch_size=2, optimizer=OptimizerConfig(**opt))
+    assert gcfg.head_dim == 128
+    print("train case head_dim 128", flush=True)
+    windows = om.synthetic_windows(11, steps, 4, 128, 997)
+    state = om.init_state(ocfg, 0)
+    trainer = GPTTrainer(gcfg, seed=0)
+    for i in range(steps):
+        w = torch.from_numpy(windows[i])
+        om.train_step(state, w[:, :-1], w[:, 1:], ocfg)
+        trainer.train_step(w[:, :-1].cuda(), w[:, 1:].cuda())
+    got = trainer.history_rows()
+    want = np.asarray(state.history)
+    print("gpu   ", got.tolist(), flush=True)
+    print("oracle", want.tolist(), flush=True)
+    assert abs(got[0, 0] - want[0, 0]) <= 1e-3 * want[0, 0]
+    assert np.all(np.abs(got[:, 0] - want[:, 0]) <= 1e-2 * want[:, 0])
+    np.testing.assert_allclose(got[:, 1], want[:, 1], rtol=1e-6)
+    assert np.all(np.abs(got[:, 2] - want[:, 2]) <= 2e-2 * want[:, 2])
+
+
 def test_train_step_completep_clip_and_residual_scale_match_oracle():
     """The official parameterization (completep_fixed_tpp_v1, recipes/reference/
     config.yaml:22-30) at width multiplier 2 and depth multiplier 2 with
