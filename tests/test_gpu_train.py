@@ -110,23 +110,27 @@ def test_train_step_flce_paths_match_oracle(label, model, trainer_only):
     assert abs(ratio - 1) <= 0.1 and cos >= 0.9
 
 
-def test_train_step_head_dim_128_matches_oracle():
+@pytest.mark.parametrize("masking", [False, True])
+def test_train_step_head_dim_128_matches_oracle(masking):
     """A 2-layer model with 2 heads of 128 (d_model 256): the trainer's
     attention runs the head_dim-128 kernels on the interleaved qkv rows, with
-    the RoPE VJP fused into the backward; history against the oracle's step."""
+    the RoPE VJP fused into the backward (and, with document masking, the
+    segment-id path); history against the oracle's step."""
     from gptrig.optim import OptimizerConfig
     from gptrig.train import GPTConfig, GPTTrainer
 
     steps = 3
     common = dict(layers=2, heads=2, d_model=256, vocab_size=1000, semantic_vocab_size=997, seq_len=128,
                   batch_size=4, base_width=256, base_depth=2, attention_scale="inverse_sqrt_head_dim",
-                  embeddings="untied")
+                  embeddings="untied", document_masking=masking, document_boundary_token=7)
     opt = dict(learning_rate=2.0 ** -8, steps=steps, warmup_steps=1)
     ocfg = om.Config(**common, attention_backend="flash", optimizer=oopt.OptimizerConfig(**opt))
     gcfg = GPTConfig(**common, micro_batch_size=2, optimizer=OptimizerConfig(**opt))
     assert gcfg.head_dim == 128
-    print("train case head_dim 128", flush=True)
+    print(f"train case head_dim 128, document masking {masking}", flush=True)
     windows = om.synthetic_windows(11, steps, 4, 128, 997)
+    if masking:
+        windows[:, :, ::29] = 7  # document boundaries
     state = om.init_state(ocfg, 0)
     trainer = GPTTrainer(gcfg, seed=0)
     for i in range(steps):
